@@ -1,0 +1,265 @@
+/*
+ * rkv.h -- C ABI of the MI355X (gfx950) paged Q8_0 KV-cache hot path.
+ *
+ * Four device operations sit behind this boundary:
+ *   - quantize-and-append of K/V rows into Q8_0 pages through block tables;
+ *   - paged flash-decode (GQA, in-register dequant, online softmax,
+ *     split-K partitions) and the causal multi-query verify variant;
+ *   - the split-K log-sum-exp combine;
+ *   - bit-exact export (gather) and import of pages in the reference's
+ *     contiguous row layout.
+ * plus the host-side page allocator and per-sequence block tables that
+ * drive them.
+ *
+ * Reference interfaces replaced (paths under leoinfer/remora-lab):
+ *   har/crates/har-serve/src/attention.rs:25-250   (Rust operator API)
+ *   har/shaders/flash_decode_q8.comp:34-52          (kernel ABI)
+ *   har/crates/har-vulkan/src/lib.rs:17-56, 236, 540-617, 1673-1777
+ *                                                   (device/queue/error API)
+ * The reference has no block table, page pool, split-K or verify kernel;
+ * those entry points extend its API in the same style.
+ *
+ * Conventions (mirroring HarError / NativeRequired, har-vulkan/src/lib.rs:17-56,
+ * har-runtime/src/policy.rs:18-48):
+ *   - every call returns rkv_status; 0 is success;
+ *   - failures never fall back to another implementation; the message of
+ *     the last failure on the calling thread is rkv_last_error();
+ *   - device pointers are plain pointers into device memory; streams are
+ *     hipStream_t passed as void* (NULL = the legacy default stream);
+ *   - calls on one pool are not thread-safe; kernels are enqueued
+ *     asynchronously and device-side faults (bad block-table entries,
+ *     positions beyond capacity) are reported by rkv_ctx_sync().
+ */
+#ifndef RKV_H
+#define RKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef int32_t rkv_status;
+enum {
+  RKV_OK = 0,
+  RKV_ERR_INVALID_ARG = -1,    /* HarError::argument (har-vulkan/src/lib.rs:547-552) */
+  RKV_ERR_OUT_OF_PAGES = -2,   /* capacity exhausted (har-native-qwen3.rs:657-660) */
+  RKV_ERR_BAD_BLOCK_TABLE = -3,/* page id / position outside the pool */
+  RKV_ERR_UNSUPPORTED = -4,    /* head_dim, page size or dtype not built */
+  RKV_ERR_DEVICE = -5,         /* HIP runtime error (HarError.result) */
+  RKV_ERR_CAPACITY = -6        /* sequence longer than its block-table row */
+};
+
+enum { RKV_F32 = 0, RKV_BF16 = 1 };                 /* element types */
+enum { RKV_Q8_CANONICAL = 0, RKV_Q8_HARSERVE = 1 }; /* quantization rules */
+enum { RKV_K = 0, RKV_V = 1 };                      /* cache kinds */
+
+/* ---- errors / version ------------------------------------------------------ */
+/* Last error of the calling thread, "operation: message"; mirrors
+ * HarError{operation,message} (har-vulkan/src/lib.rs:19-56). */
+const char *rkv_last_error(void);
+const char *rkv_version(void);
+
+/* ---- device context ---------------------------------------------------------
+ * Replaces Device::open + create_queue (har-vulkan/src/lib.rs:236, 618).
+ * Holds the device index and a device-side fault word that kernels set when
+ * they meet a bad block-table entry; rkv_ctx_sync() waits for `stream`,
+ * reads and clears that word (ComputeTicket::wait, lib.rs:2154-2201). */
+typedef struct rkv_ctx rkv_ctx;
+rkv_status rkv_ctx_create(int32_t device, rkv_ctx **out);
+rkv_status rkv_ctx_destroy(rkv_ctx *ctx);
+rkv_status rkv_ctx_sync(rkv_ctx *ctx, void *stream);
+
+/* ---- geometry of one layer's page pool ------------------------------------
+ * kv_heads, head_dim (128 or 256; attention.rs:17 fixes 256), page_tokens
+ * (16, 32, 64, 128 or 256), num_pages.  A Q8_0 row of head_dim values is
+ * head_dim/32 blocks of [f16 scale][32 x int8] (attention.rs:17-21,
+ * r4kv/src/quant.rs:1-12). */
+typedef struct rkv_kv_geometry {
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t page_tokens;
+  int32_t num_pages;
+} rkv_kv_geometry;
+rkv_status rkv_geometry_check(const rkv_kv_geometry *g);
+/* Bytes of one page (all kv heads, K and V) and of the reference row
+ * (head_dim/32*34; attention.rs:21, har-kv/src/geometry.rs:81-94). */
+size_t rkv_page_bytes(const rkv_kv_geometry *g);
+size_t rkv_row_bytes(int32_t head_dim);
+
+/* ---- page allocator and block tables (host) --------------------------------
+ * The reference has no physical page allocator (har-kv/src/page.rs:100-140
+ * keeps PhysicalPageLocation = None).  Nearest
+ * analogue: VramSlotTable::reserve (har-residency/src/manager.rs:110-157).
+ * Pages come from a free list whose initial order is a seeded permutation
+ * of [0, num_pages); freed pages return to the top of the list. */
+typedef struct rkv_alloc_desc {
+  int32_t num_pages;
+  int32_t page_tokens;
+  int32_t max_seqs;
+  int32_t max_pages_per_seq;
+  uint64_t free_list_seed;
+} rkv_alloc_desc;
+typedef struct rkv_alloc rkv_alloc;
+rkv_status rkv_alloc_create(const rkv_alloc_desc *desc, rkv_alloc **out);
+rkv_status rkv_alloc_destroy(rkv_alloc *a);
+/* Grow `seq` to new_len tokens (new_len >= current length), taking whole
+ * pages from the free list; all-or-nothing on RKV_ERR_OUT_OF_PAGES. */
+rkv_status rkv_seq_reserve(rkv_alloc *a, int32_t seq, int32_t new_len);
+/* Roll `seq` back to new_len tokens, returning pages past ceil(new_len /
+ * page_tokens) (speculative rollback, har-execution/src/speculation.rs:55,172). */
+rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len);
+rkv_status rkv_seq_free(rkv_alloc *a, int32_t seq);
+rkv_status rkv_seq_len(const rkv_alloc *a, int32_t seq, int32_t *len);
+rkv_status rkv_block_table_get(const rkv_alloc *a, int32_t seq, int32_t *out,
+                               int32_t cap, int32_t *n);
+rkv_status rkv_alloc_free_pages(const rkv_alloc *a, int32_t *n);
+/* Copy the whole table [max_seqs][max_pages_per_seq] (-1 = no page) and the
+ * lengths [max_seqs] to host buffers. */
+rkv_status rkv_alloc_export(const rkv_alloc *a, int32_t *tables, int32_t *lens);
+
+/* ---- operation arguments -------------------------------------------------- */
+typedef struct rkv_append_args {
+  int32_t n_rows;
+  const int32_t *seq_ids;   /* device [n_rows] */
+  const int32_t *positions; /* device [n_rows], token index within the sequence */
+  const void *k_src;        /* device [n_rows][kv_heads][head_dim] */
+  const void *v_src;        /* device [n_rows][kv_heads][head_dim] */
+  int32_t src_dtype;        /* RKV_F32 | RKV_BF16 */
+  int32_t rule;             /* RKV_Q8_CANONICAL | RKV_Q8_HARSERVE */
+} rkv_append_args;
+
+typedef struct rkv_decode_args {
+  int32_t batch;            /* B */
+  const int32_t *seq_ids;   /* device [B] */
+  const void *q;            /* device [B][q_len][q_heads][head_dim], 16-byte aligned */
+  int32_t q_dtype;          /* RKV_F32 | RKV_BF16 */
+  int32_t q_len;            /* 1 = decode; 2..4 = causal verify of draft rows */
+  int32_t q_heads;          /* multiple of kv_heads (attention.rs:154-157) */
+  float scale;              /* softmax scale on q.k (1.0 = attention.rs) */
+  void *out;                /* device [B][q_len][q_heads][head_dim] */
+  int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
+  int32_t partition_tokens; /* split-K partition length: a multiple of max(32,
+                               page_tokens), at most 64*page_tokens; 0 = auto */
+  int32_t max_seq_len;      /* >= every seq_lens[seq_ids[b]]; sizes the grid */
+  void *workspace;          /* device scratch for split-K partials (may be NULL
+                               when one partition covers every sequence) */
+  size_t workspace_bytes;
+} rkv_decode_args;
+
+/* ---- kernel-level entry points (explicit device pointers) -----------------
+ * pages: one layer's pool (num_pages * rkv_page_bytes).  block_tables:
+ * device int32 [n_seqs][bt_stride]; seq_lens: device int32 [n_seqs]. */
+
+/* Quantize-and-append.  Replaces q8_0_quantize (attention.rs:25-42) /
+ * r4kv::quant::encode (quant.rs:138-170) followed by the host copy into the
+ * shader's K/V buffers (har-serve-vulkan-attn-smoke.rs:62-69, 95-127). */
+rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
+                         const int32_t *block_tables, int32_t bt_stride,
+                         int32_t n_seqs, const rkv_append_args *args, void *stream);
+
+/* Paged flash-decode (+ causal verify when q_len > 1).  Replaces
+ * flash_decode_reference / flash_decode_online (attention.rs:148-215) and
+ * the flash_decode_q8.comp dispatch (har-serve-vulkan-attn-smoke.rs:149-161).
+ * With more than one partition per sequence the partials go to `workspace`
+ * and the combine runs on the same stream. */
+rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                         const int32_t *block_tables, int32_t bt_stride,
+                         const int32_t *seq_lens, int32_t n_seqs,
+                         const rkv_decode_args *args, void *stream);
+/* Workspace bytes rkv_decode_q8 needs for these arguments (0 if none). */
+size_t rkv_decode_workspace_bytes(const rkv_kv_geometry *g, const rkv_decode_args *args);
+/* Partition length rkv_decode_q8 uses for these arguments. */
+int32_t rkv_decode_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *args);
+
+/* Split-K stage alone (for parity tests): writes per-partition partials
+ * (m, l) into ml [B][q_len*q_heads][n_parts][2] and o into
+ * o [B][q_len*q_heads][n_parts][head_dim].  m is the running max of
+ * scale*log2(e)*q.k (base-2 domain); l and o are unnormalised sums of
+ * 2^(s - m) and 2^(s - m) * v.  n_parts = ceil(max_seq_len/partition_tokens). */
+rkv_status rkv_decode_q8_partials(rkv_ctx *ctx, const rkv_kv_geometry *g,
+                                  const void *pages, const int32_t *block_tables,
+                                  int32_t bt_stride, const int32_t *seq_lens,
+                                  int32_t n_seqs, const rkv_decode_args *args,
+                                  float *ml, float *o, void *stream);
+/* Log-sum-exp combine of the partials above (attention.rs:205-212 algebra):
+ * M = max m_p, L = sum l_p 2^(m_p-M), out = sum o_p 2^(m_p-M) / L; L == 0
+ * gives zeros (flash_decode_q8.comp:144-148).  Only the first
+ * ceil(seq_lens[seq_ids[b]]/partition_tokens) partitions of entry b are read. */
+rkv_status rkv_splitk_combine(rkv_ctx *ctx, const float *ml, const float *o,
+                              int32_t batch, int32_t rows, int32_t n_parts,
+                              int32_t head_dim, const int32_t *seq_ids,
+                              const int32_t *seq_lens, int32_t n_seqs,
+                              int32_t partition_tokens, void *out, int32_t out_dtype,
+                              void *stream);
+
+/* Export seq's K or V cache in the reference contiguous layout
+ * [kv_heads][len][head_dim/32*34] bytes (what flash_decode_reference reads,
+ * attention.rs:144-147; row_to_words is a reinterpretation, :115-120). */
+rkv_status rkv_gather_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                         const int32_t *block_table, int32_t len, int32_t kind,
+                         uint8_t *out, void *stream);
+/* Inverse of rkv_gather_q8: write reference rows into the pages. */
+rkv_status rkv_import_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
+                         const int32_t *block_table, int32_t len, int32_t kind,
+                         const uint8_t *rows, void *stream);
+
+/* Batch f32 -> binary16 bits with the device encoder of one rule
+ * (RKV_Q8_CANONICAL = r4kv/src/f16.rs:27-86, RKV_Q8_HARSERVE =
+ * attention.rs:45-76); used to pin the scale encoder over many inputs. */
+rkv_status rkv_f32_to_f16(rkv_ctx *ctx, const float *in, uint16_t *out, int64_t n,
+                          int32_t rule, void *stream);
+
+/* Drop-in for the flash_decode_q8.comp ABI (:36-52): contiguous K/V words
+ * [kv_heads][seq_len][head_dim/32*34/4], query f32 [q_heads][head_dim],
+ * out f32 [q_heads][head_dim], no softmax scale, l == 0 -> zeros.
+ * `scratch` must hold rkv_flash_decode_scratch_bytes(); the rows are
+ * imported into a scratch pool and decoded there. */
+typedef struct rkv_flash_decode_params {
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t seq_len;
+  int32_t chunk;    /* accepted for API parity (attention.rs:128-130) */
+  int32_t head_dim;
+} rkv_flash_decode_params;
+size_t rkv_flash_decode_scratch_bytes(const rkv_flash_decode_params *p);
+rkv_status rkv_flash_decode_q8(rkv_ctx *ctx, const rkv_flash_decode_params *p,
+                               const uint32_t *k_words, const uint32_t *v_words,
+                               const float *query, float *out, void *scratch,
+                               void *stream);
+
+/* ---- pool: device pages for `layers` layers + allocator + device tables ----
+ * The operator-level API a serving adapter (BatchStepModel, adapter.rs:28-72)
+ * would hold per model.  Block-table edits made through the allocator are
+ * uploaded by rkv_pool_sync_tables() before the next launch. */
+typedef struct rkv_pool_desc {
+  int32_t layers;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t page_tokens;
+  int32_t num_pages;
+  int32_t max_seqs;
+  int32_t max_pages_per_seq;
+  uint64_t free_list_seed;
+} rkv_pool_desc;
+typedef struct rkv_pool rkv_pool;
+rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **out);
+rkv_status rkv_pool_destroy(rkv_pool *pool);
+rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
+rkv_status rkv_pool_sync_tables(rkv_pool *pool, void *stream);
+/* Device pointers owned by the pool. */
+void *rkv_pool_layer_pages(rkv_pool *pool, int32_t layer);
+const int32_t *rkv_pool_block_tables(rkv_pool *pool); /* [max_seqs][max_pages_per_seq] */
+const int32_t *rkv_pool_seq_lens(rkv_pool *pool);     /* [max_seqs] */
+rkv_status rkv_pool_append(rkv_pool *pool, int32_t layer, const rkv_append_args *args,
+                           void *stream);
+rkv_status rkv_pool_decode(rkv_pool *pool, int32_t layer, const rkv_decode_args *args,
+                           void *stream);
+rkv_status rkv_pool_gather(rkv_pool *pool, int32_t layer, int32_t seq, int32_t kind,
+                           uint8_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* RKV_H */

@@ -1,0 +1,403 @@
+"""Python binding of librkv.so, the C ABI in include/rkv.h.
+
+The paged Q8_0 KV-cache hot path runs entirely in the HIP kernels behind that
+ABI; this module only forwards device pointers (torch tensors on a ROCm
+device) and turns non-zero statuses into RkvError, mirroring the reference's
+fail-closed HarError convention (har/crates/har-vulkan/src/lib.rs:17-56).
+There is no CPU fallback: without the built library every call raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librkv.so")
+HEADER = os.path.join(HERE, "..", "include", "rkv.h")
+
+OK = 0
+ERR_INVALID_ARG = -1
+ERR_OUT_OF_PAGES = -2
+ERR_BAD_BLOCK_TABLE = -3
+ERR_UNSUPPORTED = -4
+ERR_DEVICE = -5
+ERR_CAPACITY = -6
+
+F32, BF16 = 0, 1
+Q8_CANONICAL, Q8_HARSERVE = 0, 1
+K, V = 0, 1
+
+_STATUS_NAMES = {0: "OK", -1: "INVALID_ARG", -2: "OUT_OF_PAGES", -3: "BAD_BLOCK_TABLE",
+                 -4: "UNSUPPORTED", -5: "DEVICE", -6: "CAPACITY"}
+
+
+class RkvError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{_STATUS_NAMES.get(status, status)}: {message}")
+        self.status = status
+        self.message = message
+
+
+P = C.c_void_p
+I32P = C.POINTER(C.c_int32)
+
+
+class Geometry(C.Structure):
+    _fields_ = [("kv_heads", C.c_int32), ("head_dim", C.c_int32), ("page_tokens", C.c_int32),
+                ("num_pages", C.c_int32)]
+
+
+class AllocDesc(C.Structure):
+    _fields_ = [("num_pages", C.c_int32), ("page_tokens", C.c_int32), ("max_seqs", C.c_int32),
+                ("max_pages_per_seq", C.c_int32), ("free_list_seed", C.c_uint64)]
+
+
+class AppendArgs(C.Structure):
+    _fields_ = [("n_rows", C.c_int32), ("seq_ids", P), ("positions", P), ("k_src", P),
+                ("v_src", P), ("src_dtype", C.c_int32), ("rule", C.c_int32)]
+
+
+class DecodeArgs(C.Structure):
+    _fields_ = [("batch", C.c_int32), ("seq_ids", P), ("q", P), ("q_dtype", C.c_int32),
+                ("q_len", C.c_int32), ("q_heads", C.c_int32), ("scale", C.c_float),
+                ("out", P), ("out_dtype", C.c_int32), ("partition_tokens", C.c_int32),
+                ("max_seq_len", C.c_int32), ("workspace", P), ("workspace_bytes", C.c_size_t)]
+
+
+class FlashDecodeParams(C.Structure):
+    _fields_ = [("q_heads", C.c_int32), ("kv_heads", C.c_int32), ("seq_len", C.c_int32),
+                ("chunk", C.c_int32), ("head_dim", C.c_int32)]
+
+
+class PoolDesc(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("page_tokens", C.c_int32), ("num_pages", C.c_int32), ("max_seqs", C.c_int32),
+                ("max_pages_per_seq", C.c_int32), ("free_list_seed", C.c_uint64)]
+
+
+_SIGS = {
+    "rkv_last_error": (C.c_char_p, []),
+    "rkv_version": (C.c_char_p, []),
+    "rkv_ctx_create": (C.c_int32, [C.c_int32, C.POINTER(P)]),
+    "rkv_ctx_destroy": (C.c_int32, [P]),
+    "rkv_ctx_sync": (C.c_int32, [P, P]),
+    "rkv_geometry_check": (C.c_int32, [C.POINTER(Geometry)]),
+    "rkv_page_bytes": (C.c_size_t, [C.POINTER(Geometry)]),
+    "rkv_row_bytes": (C.c_size_t, [C.c_int32]),
+    "rkv_alloc_create": (C.c_int32, [C.POINTER(AllocDesc), C.POINTER(P)]),
+    "rkv_alloc_destroy": (C.c_int32, [P]),
+    "rkv_seq_reserve": (C.c_int32, [P, C.c_int32, C.c_int32]),
+    "rkv_seq_truncate": (C.c_int32, [P, C.c_int32, C.c_int32]),
+    "rkv_seq_free": (C.c_int32, [P, C.c_int32]),
+    "rkv_seq_len": (C.c_int32, [P, C.c_int32, I32P]),
+    "rkv_block_table_get": (C.c_int32, [P, C.c_int32, I32P, C.c_int32, I32P]),
+    "rkv_alloc_free_pages": (C.c_int32, [P, I32P]),
+    "rkv_alloc_export": (C.c_int32, [P, P, P]),
+    "rkv_append_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32,
+                                  C.POINTER(AppendArgs), P]),
+    "rkv_decode_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P, C.c_int32,
+                                  C.POINTER(DecodeArgs), P]),
+    "rkv_decode_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
+    "rkv_decode_partition_tokens": (C.c_int32, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
+    "rkv_decode_q8_partials": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P,
+                                           C.c_int32, C.POINTER(DecodeArgs), P, P, P]),
+    "rkv_splitk_combine": (C.c_int32, [P, P, P, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                       P, P, C.c_int32, C.c_int32, P, C.c_int32, P]),
+    "rkv_gather_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32, P, P]),
+    "rkv_import_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32, P, P]),
+    "rkv_f32_to_f16": (C.c_int32, [P, P, P, C.c_int64, C.c_int32, P]),
+    "rkv_flash_decode_scratch_bytes": (C.c_size_t, [C.POINTER(FlashDecodeParams)]),
+    "rkv_flash_decode_q8": (C.c_int32, [P, C.POINTER(FlashDecodeParams), P, P, P, P, P, P]),
+    "rkv_pool_create": (C.c_int32, [P, C.POINTER(PoolDesc), C.POINTER(P)]),
+    "rkv_pool_destroy": (C.c_int32, [P]),
+    "rkv_pool_allocator": (P, [P]),
+    "rkv_pool_sync_tables": (C.c_int32, [P, P]),
+    "rkv_pool_layer_pages": (P, [P, C.c_int32]),
+    "rkv_pool_block_tables": (P, [P]),
+    "rkv_pool_seq_lens": (P, [P]),
+    "rkv_pool_append": (C.c_int32, [P, C.c_int32, C.POINTER(AppendArgs), P]),
+    "rkv_pool_decode": (C.c_int32, [P, C.c_int32, C.POINTER(DecodeArgs), P]),
+    "rkv_pool_gather": (C.c_int32, [P, C.c_int32, C.c_int32, C.c_int32, P, P]),
+}
+
+_lib = None
+
+
+def header_symbols() -> list[str]:
+    """Function names declared in include/rkv.h."""
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(rkv_[a-z0-9_]+)\s*\(", text)))
+
+
+def lib():
+    """Load librkv.so; raise if it was not built (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise RkvError(status, lib().rkv_last_error().decode())
+
+
+def _ptr(t) -> P:
+    """Device pointer of a torch tensor (or an int address, or None)."""
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return P(t)
+    return P(t.data_ptr())
+
+
+def _stream(s) -> P:
+    if s is None:
+        import torch
+        return P(torch.cuda.current_stream().cuda_stream)
+    if isinstance(s, int):
+        return P(s)
+    return P(s.cuda_stream)
+
+
+class Ctx:
+    """Device context (replaces har-vulkan Device::open + Queue)."""
+
+    def __init__(self, device: int = 0):
+        h = P()
+        check(lib().rkv_ctx_create(device, C.byref(h)))
+        self.h = h
+        self.device = device
+
+    def sync(self, stream=None) -> None:
+        check(lib().rkv_ctx_sync(self.h, _stream(stream)))
+
+    def close(self) -> None:
+        if self.h:
+            lib().rkv_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def geometry(kv_heads: int, head_dim: int, page_tokens: int, num_pages: int) -> Geometry:
+    g = Geometry(kv_heads, head_dim, page_tokens, num_pages)
+    check(lib().rkv_geometry_check(C.byref(g)))
+    return g
+
+
+def page_bytes(g: Geometry) -> int:
+    return lib().rkv_page_bytes(C.byref(g))
+
+
+def row_bytes(head_dim: int) -> int:
+    return lib().rkv_row_bytes(head_dim)
+
+
+class Allocator:
+    """Host page allocator + block tables (rkv_alloc_*)."""
+
+    def __init__(self, num_pages, page_tokens, max_seqs, max_pages_per_seq, seed=0, handle=None):
+        self.owned = handle is None
+        if handle is None:
+            h = P()
+            d = AllocDesc(num_pages, page_tokens, max_seqs, max_pages_per_seq, seed)
+            check(lib().rkv_alloc_create(C.byref(d), C.byref(h)))
+            handle = h
+        self.h = handle
+        self.max_seqs = max_seqs
+        self.max_pages_per_seq = max_pages_per_seq
+
+    def reserve(self, seq: int, new_len: int) -> None:
+        check(lib().rkv_seq_reserve(self.h, seq, new_len))
+
+    def truncate(self, seq: int, new_len: int) -> None:
+        check(lib().rkv_seq_truncate(self.h, seq, new_len))
+
+    def free(self, seq: int) -> None:
+        check(lib().rkv_seq_free(self.h, seq))
+
+    def seq_len(self, seq: int) -> int:
+        n = C.c_int32()
+        check(lib().rkv_seq_len(self.h, seq, C.byref(n)))
+        return n.value
+
+    def block_table(self, seq: int) -> list[int]:
+        buf = (C.c_int32 * self.max_pages_per_seq)()
+        n = C.c_int32()
+        check(lib().rkv_block_table_get(self.h, seq, buf, self.max_pages_per_seq, C.byref(n)))
+        return list(buf[: n.value])
+
+    def free_pages(self) -> int:
+        n = C.c_int32()
+        check(lib().rkv_alloc_free_pages(self.h, C.byref(n)))
+        return n.value
+
+    def export(self):
+        import numpy as np
+        tables = np.empty((self.max_seqs, self.max_pages_per_seq), np.int32)
+        lens = np.empty(self.max_seqs, np.int32)
+        check(lib().rkv_alloc_export(self.h, tables.ctypes.data_as(P), lens.ctypes.data_as(P)))
+        return tables, lens
+
+    def close(self) -> None:
+        if self.owned and self.h:
+            lib().rkv_alloc_destroy(self.h)
+        self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- kernel-level operations (torch tensors on the device) -------------------
+
+def append_q8(ctx: Ctx, g: Geometry, pages, block_tables, seq_ids, positions, k_src, v_src,
+              rule: int = Q8_CANONICAL, stream=None) -> None:
+    import torch
+    bt_stride = block_tables.shape[-1]
+    n_seqs = block_tables.shape[0]
+    dtype = BF16 if k_src.dtype == torch.bfloat16 else F32
+    a = AppendArgs(seq_ids.numel(), _ptr(seq_ids), _ptr(positions), _ptr(k_src), _ptr(v_src),
+                   dtype, rule)
+    check(lib().rkv_append_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables), bt_stride,
+                              n_seqs, C.byref(a), _stream(stream)))
+
+
+def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0,
+                workspace=None) -> DecodeArgs:
+    import torch
+    B = seq_ids.numel()
+    q_heads = q.shape[-2]
+    return DecodeArgs(B, _ptr(seq_ids), _ptr(q), BF16 if q.dtype == torch.bfloat16 else F32,
+                      q_len, q_heads, scale, _ptr(out),
+                      BF16 if out.dtype == torch.bfloat16 else F32, partition_tokens,
+                      max_seq_len, _ptr(workspace),
+                      0 if workspace is None else workspace.numel() * workspace.element_size())
+
+
+def decode_workspace_bytes(g: Geometry, a: DecodeArgs) -> int:
+    return lib().rkv_decode_workspace_bytes(C.byref(g), C.byref(a))
+
+
+def decode_partition_tokens(g: Geometry, a: DecodeArgs) -> int:
+    return lib().rkv_decode_partition_tokens(C.byref(g), C.byref(a))
+
+
+def decode_q8(ctx: Ctx, g: Geometry, pages, block_tables, seq_lens, a: DecodeArgs,
+              stream=None) -> None:
+    check(lib().rkv_decode_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables),
+                              block_tables.shape[-1], _ptr(seq_lens), seq_lens.numel(),
+                              C.byref(a), _stream(stream)))
+
+
+def decode_q8_partials(ctx: Ctx, g: Geometry, pages, block_tables, seq_lens, a: DecodeArgs,
+                       ml, o, stream=None) -> None:
+    check(lib().rkv_decode_q8_partials(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables),
+                                       block_tables.shape[-1], _ptr(seq_lens), seq_lens.numel(),
+                                       C.byref(a), _ptr(ml), _ptr(o), _stream(stream)))
+
+
+def splitk_combine(ctx: Ctx, ml, o, batch, rows, n_parts, head_dim, seq_ids, seq_lens,
+                   partition_tokens, out, stream=None) -> None:
+    import torch
+    check(lib().rkv_splitk_combine(ctx.h, _ptr(ml), _ptr(o), batch, rows, n_parts, head_dim,
+                                   _ptr(seq_ids), _ptr(seq_lens), seq_lens.numel(),
+                                   partition_tokens, _ptr(out),
+                                   BF16 if out.dtype == torch.bfloat16 else F32,
+                                   _stream(stream)))
+
+
+def gather_q8(ctx: Ctx, g: Geometry, pages, block_table, length: int, kind: int, out,
+              stream=None) -> None:
+    check(lib().rkv_gather_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_table), length, kind,
+                              _ptr(out), _stream(stream)))
+
+
+def import_q8(ctx: Ctx, g: Geometry, pages, block_table, length: int, kind: int, rows,
+              stream=None) -> None:
+    check(lib().rkv_import_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_table), length, kind,
+                              _ptr(rows), _stream(stream)))
+
+
+def f32_to_f16(ctx: Ctx, x, out, rule: int, stream=None) -> None:
+    check(lib().rkv_f32_to_f16(ctx.h, _ptr(x), _ptr(out), x.numel(), rule, _stream(stream)))
+
+
+def flash_decode_scratch_bytes(p: FlashDecodeParams) -> int:
+    return lib().rkv_flash_decode_scratch_bytes(C.byref(p))
+
+
+def flash_decode_q8(ctx: Ctx, p: FlashDecodeParams, k_words, v_words, query, out, scratch,
+                    stream=None) -> None:
+    check(lib().rkv_flash_decode_q8(ctx.h, C.byref(p), _ptr(k_words), _ptr(v_words),
+                                    _ptr(query), _ptr(out), _ptr(scratch), _stream(stream)))
+
+
+class Pool:
+    """Device pages for `layers` layers + allocator + device block tables."""
+
+    def __init__(self, ctx: Ctx, layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
+                 max_pages_per_seq, seed=0):
+        self.ctx = ctx
+        d = PoolDesc(layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
+                     max_pages_per_seq, seed)
+        h = P()
+        check(lib().rkv_pool_create(ctx.h, C.byref(d), C.byref(h)))
+        self.h = h
+        self.desc = d
+        self.geometry = Geometry(kv_heads, head_dim, page_tokens, num_pages)
+        self.alloc = Allocator(num_pages, page_tokens, max_seqs, max_pages_per_seq,
+                               handle=P(lib().rkv_pool_allocator(h)))
+
+    def sync_tables(self, stream=None) -> None:
+        check(lib().rkv_pool_sync_tables(self.h, _stream(stream)))
+
+    def layer_pages(self, layer: int) -> int:
+        return lib().rkv_pool_layer_pages(self.h, layer)
+
+    def block_tables_ptr(self) -> int:
+        return lib().rkv_pool_block_tables(self.h)
+
+    def seq_lens_ptr(self) -> int:
+        return lib().rkv_pool_seq_lens(self.h)
+
+    def append(self, layer, seq_ids, positions, k_src, v_src, rule=Q8_CANONICAL,
+               stream=None) -> None:
+        import torch
+        dtype = BF16 if k_src.dtype == torch.bfloat16 else F32
+        a = AppendArgs(seq_ids.numel(), _ptr(seq_ids), _ptr(positions), _ptr(k_src),
+                       _ptr(v_src), dtype, rule)
+        check(lib().rkv_pool_append(self.h, layer, C.byref(a), _stream(stream)))
+
+    def decode(self, layer, a: DecodeArgs, stream=None) -> None:
+        check(lib().rkv_pool_decode(self.h, layer, C.byref(a), _stream(stream)))
+
+    def gather(self, layer, seq, kind, out, stream=None) -> None:
+        check(lib().rkv_pool_gather(self.h, layer, seq, kind, _ptr(out), _stream(stream)))
+
+    def close(self) -> None:
+        if self.h:
+            self.alloc.h = None
+            lib().rkv_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,205 @@
+// rkv_append.hip -- quantize-and-append of K/V rows into Q8_0 pages, the
+// bit-exact gather/import between pages and reference rows, and a batch
+// f16 encoder (gfx950).
+//
+// Quantization rules (bit-exact with the CPU reference):
+//   canonical (har/crates/r4kv/src/quant.rs:45-90): amax = max|v| over the
+//     32-value group, d = amax/127 (f32, IEEE division), inv = 1/d,
+//     q = clamp(round_half_away(v*inv), -127, 127), scale = f16_rtne(d);
+//   har-serve (har/crates/har-serve/src/attention.rs:25-42): same d,
+//     q = clamp(round_half_away(v/d)), scale = attention.rs's f16 encoder.
+// hipcc keeps f32 division correctly rounded (flag set by the build) and
+// this file has no a*b+c patterns, so contraction cannot change a result.
+#include "rkv_launch.h"
+
+namespace rkv {
+
+namespace {
+
+// One group of 8 lanes quantizes one 32-value block; lane `sub` owns values
+// 4*sub..4*sub+3.  The block index enumerates (row, kv_head, kind, block).
+__global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
+  const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
+  const int32_t D = a.g.head_dim;
+  const int32_t NB = D >> 5;
+  const uint32_t nblocks = (uint32_t)a.n_rows * (uint32_t)a.g.kv_heads * 2u * (uint32_t)NB;
+  const uint32_t blk = tid >> 3;
+  const int32_t sub = (int32_t)(tid & 7u);
+  // Every lane takes part in the shuffles; out-of-range lanes use zeros.
+  const bool live = blk < nblocks;
+  const uint32_t blkc = live ? blk : 0u;
+  const int32_t b = (int32_t)(blkc % (uint32_t)NB);
+  uint32_t t = blkc / (uint32_t)NB;
+  const int32_t kind = (int32_t)(t & 1u);
+  t >>= 1;
+  const int32_t kvh = (int32_t)(t % (uint32_t)a.g.kv_heads);
+  const int32_t row = (int32_t)(t / (uint32_t)a.g.kv_heads);
+
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (live) {
+    const uint64_t off =
+        ((uint64_t)row * (uint64_t)a.g.kv_heads + (uint64_t)kvh) * (uint64_t)D + (uint64_t)(b * 32 + sub * 4);
+    const void *src = kind == 0 ? a.k_src : a.v_src;
+    if (a.src_bf16) {
+      const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(src) + off);
+      v[0] = bf16_bits_to_f32((uint16_t)(w.x & 0xffffu));
+      v[1] = bf16_bits_to_f32((uint16_t)(w.x >> 16));
+      v[2] = bf16_bits_to_f32((uint16_t)(w.y & 0xffffu));
+      v[3] = bf16_bits_to_f32((uint16_t)(w.y >> 16));
+    } else {
+      const float4 w = *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + off);
+      v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+    }
+  }
+  // amax ignores NaN (quant.rs:49-55 compares `a > amax`; attention.rs:29
+  // uses f32::max) -- both equal this.
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float x = fabsf(v[i]);
+    amax = x > amax ? x : amax;
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  if (!live) return;
+
+  const float d = amax == 0.0f ? 0.0f : amax / 127.0f;
+  uint32_t codes = 0;
+  uint16_t scale;
+  if (a.rule == 0) {
+    const float inv = d == 0.0f ? 0.0f : 1.0f / d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      codes |= ((uint32_t)(uint8_t)(int8_t)q8_code(roundf(v[i] * inv))) << (8 * i);
+    scale = f16_rtne(d);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int32_t q = d == 0.0f ? 0 : q8_code(roundf(v[i] / d));
+      codes |= ((uint32_t)(uint8_t)(int8_t)q) << (8 * i);
+    }
+    scale = f16_harserve(d);
+  }
+
+  const int32_t seq = a.seq_ids[row];
+  const int32_t pos = a.positions[row];
+  if (seq < 0 || seq >= a.n_seqs) {
+    if (sub == 0) atomicOr(a.fault, FAULT_BAD_SEQ);
+    return;
+  }
+  if (pos < 0 || pos / a.g.page_tokens >= a.bt_stride) {
+    if (sub == 0) atomicOr(a.fault, FAULT_BAD_POSITION);
+    return;
+  }
+  const int32_t page = a.bt[(int64_t)seq * a.bt_stride + pos / a.g.page_tokens];
+  if (page < 0 || page >= a.g.num_pages) {
+    if (sub == 0) atomicOr(a.fault, FAULT_BAD_PAGE);
+    return;
+  }
+  const int32_t slot = pos % a.g.page_tokens;
+  uint8_t *region = a.pages + region_base(a.g, page, kvh, kind);
+  const int32_t dim0 = b * 32 + sub * 4;
+  if (kind == 0) {
+    *reinterpret_cast<uint32_t *>(region + code_offset(a.g, 0, slot, dim0)) = codes;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) region[code_offset(a.g, 1, slot, dim0 + i)] = (uint8_t)(codes >> (8 * i));
+  }
+  if (sub == 0) *reinterpret_cast<uint16_t *>(region + scale_offset(a.g, slot, b)) = scale;
+}
+
+// One thread per (kv_head, position, block): 34 reference-row bytes.
+__global__ __launch_bounds__(256) void gather_kernel(Geo g, const uint8_t *pages, const int32_t *bt,
+                                                     int32_t len, int32_t kind, uint8_t *rows,
+                                                     int32_t *fault) {
+  const int32_t NB = g.head_dim >> 5;
+  const int64_t n = (int64_t)g.kv_heads * len * NB;
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (tid >= n) return;
+  const int32_t b = (int32_t)(tid % NB);
+  const int64_t t = tid / NB;
+  const int32_t pos = (int32_t)(t % len);
+  const int32_t kvh = (int32_t)(t / len);
+  const int32_t page = bt[pos / g.page_tokens];
+  if (page < 0 || page >= g.num_pages) {
+    atomicOr(fault, FAULT_BAD_PAGE);
+    return;
+  }
+  const int32_t slot = pos % g.page_tokens;
+  const uint8_t *region = pages + region_base(g, page, kvh, kind);
+  uint8_t *dst = rows + ((int64_t)kvh * len + pos) * (NB * 34) + b * 34;
+  const uint16_t sc = *reinterpret_cast<const uint16_t *>(region + scale_offset(g, slot, b));
+  dst[0] = (uint8_t)(sc & 0xffu);
+  dst[1] = (uint8_t)(sc >> 8);
+  for (int i = 0; i < 32; ++i) dst[2 + i] = region[code_offset(g, kind, slot, b * 32 + i)];
+}
+
+__global__ __launch_bounds__(256) void import_kernel(Geo g, uint8_t *pages, const int32_t *bt,
+                                                     int32_t len, int32_t kind, const uint8_t *rows,
+                                                     int32_t *fault) {
+  const int32_t NB = g.head_dim >> 5;
+  const int64_t n = (int64_t)g.kv_heads * len * NB;
+  const int64_t tid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (tid >= n) return;
+  const int32_t b = (int32_t)(tid % NB);
+  const int64_t t = tid / NB;
+  const int32_t pos = (int32_t)(t % len);
+  const int32_t kvh = (int32_t)(t / len);
+  const int32_t page = bt[pos / g.page_tokens];
+  if (page < 0 || page >= g.num_pages) {
+    atomicOr(fault, FAULT_BAD_PAGE);
+    return;
+  }
+  const int32_t slot = pos % g.page_tokens;
+  uint8_t *region = pages + region_base(g, page, kvh, kind);
+  const uint8_t *src = rows + ((int64_t)kvh * len + pos) * (NB * 34) + b * 34;
+  *reinterpret_cast<uint16_t *>(region + scale_offset(g, slot, b)) =
+      (uint16_t)(src[0] | ((uint16_t)src[1] << 8));
+  for (int i = 0; i < 32; ++i) region[code_offset(g, kind, slot, b * 32 + i)] = src[2 + i];
+}
+
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float *in, uint16_t *out, int64_t n,
+                                                         int32_t rule) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  out[i] = rule == 0 ? f16_rtne(in[i]) : f16_harserve(in[i]);
+}
+
+inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 255) / 256); }
+
+}  // namespace
+
+hipError_t launch_append(const AppendLaunch &a, hipStream_t s) {
+  const int64_t threads = (int64_t)a.n_rows * a.g.kv_heads * 2 * (a.g.head_dim / 32) * 8;
+  if (threads == 0) return hipSuccess;
+  hipLaunchKernelGGL(append_kernel, dim3(grid_for(threads)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const Geo &g, const uint8_t *pages, const int32_t *bt, int32_t len,
+                         int32_t kind, uint8_t *rows, int32_t *fault, hipStream_t s) {
+  const int64_t n = (int64_t)g.kv_heads * len * (g.head_dim / 32);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n)), dim3(256), 0, s, g, pages, bt, len, kind,
+                     rows, fault);
+  return hipGetLastError();
+}
+
+hipError_t launch_import(const Geo &g, uint8_t *pages, const int32_t *bt, int32_t len,
+                         int32_t kind, const uint8_t *rows, int32_t *fault, hipStream_t s) {
+  const int64_t n = (int64_t)g.kv_heads * len * (g.head_dim / 32);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(import_kernel, dim3(grid_for(n)), dim3(256), 0, s, g, pages, bt, len, kind,
+                     rows, fault);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_to_f16(const float *in, uint16_t *out, int64_t n, int32_t rule,
+                             hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, s, in, out, n, rule);
+  return hipGetLastError();
+}
+
+}  // namespace rkv

@@ -1,0 +1,151 @@
+// rkv_device.h -- device-side building blocks shared by the gfx950 kernels:
+// the page layout in HBM, the binary16 scale encoders and the Q8_0 group
+// quantizer.  Everything here is bit-exact integer/IEEE code; nothing uses
+// fast-math.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rkv {
+
+// ---------------------------------------------------------------------------
+// Page layout (one layer of the pool).
+//
+// A page holds page_tokens token slots for every kv head, K then V:
+//   page   = [kv_head][kind K|V][region]
+//   region = codes (page_tokens*D bytes) then scales (page_tokens*D/32 f16)
+//   K codes : [slot][dim]                 -- the reference row order
+//   V codes : [slot/TT][dim][slot%TT]     -- dim-major inside 32-slot tiles
+//   scales  : [slot/TT][block][slot%TT]   -- K and V alike
+// with TT = min(32, page_tokens).  The bytes of one reference row
+// (har/crates/har-serve/src/attention.rs:17-21: per 32-value block an LE f16
+// scale then 32 int8 codes) are a fixed permutation of these; rkv_gather_q8
+// applies the inverse.  Why: a 32-token tile of K codes, of V codes and of
+// each scale array is a contiguous, 16-byte aligned run, so the decode
+// kernel streams it with full 128-byte lines, the QK product reads K rows
+// and the PV product reads V columns without byte shuffles.
+// ---------------------------------------------------------------------------
+struct Geo {
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t page_tokens;
+  int32_t num_pages;
+};
+
+__host__ __device__ inline int32_t tile_tokens(int32_t page_tokens) {
+  return page_tokens < 32 ? page_tokens : 32;
+}
+__host__ __device__ inline uint64_t region_bytes(const Geo &g) {
+  return (uint64_t)g.page_tokens * (uint64_t)g.head_dim * 17u / 16u;
+}
+__host__ __device__ inline uint64_t page_bytes(const Geo &g) {
+  return (uint64_t)g.kv_heads * 2u * region_bytes(g);
+}
+__host__ __device__ inline uint64_t region_base(const Geo &g, int32_t page, int32_t kvh,
+                                                int32_t kind) {
+  return (uint64_t)page * page_bytes(g) + (uint64_t)(kvh * 2 + kind) * region_bytes(g);
+}
+// byte offset of code (slot, dim) inside a region of `kind`
+__host__ __device__ inline uint32_t code_offset(const Geo &g, int32_t kind, int32_t slot,
+                                                int32_t dim) {
+  const uint32_t D = (uint32_t)g.head_dim;
+  if (kind == 0) return (uint32_t)slot * D + (uint32_t)dim;
+  const uint32_t TT = (uint32_t)tile_tokens(g.page_tokens);
+  return ((uint32_t)slot / TT) * D * TT + (uint32_t)dim * TT + (uint32_t)slot % TT;
+}
+// byte offset of the f16 scale of (slot, block) inside a region
+__host__ __device__ inline uint32_t scale_offset(const Geo &g, int32_t slot, int32_t block) {
+  const uint32_t D = (uint32_t)g.head_dim;
+  const uint32_t TT = (uint32_t)tile_tokens(g.page_tokens);
+  return (uint32_t)g.page_tokens * D +
+         2u * (((uint32_t)slot / TT) * (D / 32u) * TT + (uint32_t)block * TT +
+               (uint32_t)slot % TT);
+}
+
+// Device-side fault word bits (read back by rkv_ctx_sync).
+enum : int32_t { FAULT_BAD_PAGE = 1, FAULT_BAD_POSITION = 2, FAULT_BAD_SEQ = 4 };
+
+// ---------------------------------------------------------------------------
+// binary16 encoders.
+// ---------------------------------------------------------------------------
+
+// IEEE binary16, round to nearest even, subnormals and carries handled:
+// the encoder of har/crates/r4kv/src/f16.rs:27-86.
+__host__ __device__ inline uint16_t f16_rtne(float v) {
+  uint32_t x = __builtin_bit_cast(uint32_t, v);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  int32_t bexp = (int32_t)((x >> 23) & 0xffu);
+  uint32_t frac = x & 0x7fffffu;
+  if (bexp == 0xff) return (uint16_t)(sign | 0x7c00u | (frac ? 0x200u : 0u));
+  int32_t e = bexp - 127;
+  if (e > 15) return (uint16_t)(sign | 0x7c00u);
+  uint32_t m = frac | 0x800000u;
+  if (e >= -14) {
+    // keep 11 significant bits; round on the 13 dropped bits
+    uint32_t r = (m >> 13) + (((m & 0x1fffu) > 0x1000u) ||
+                              ((m & 0x1fffu) == 0x1000u && ((m >> 13) & 1u)));
+    uint32_t h = ((uint32_t)(e + 15) << 10) + (r - 0x400u);  // carry flows into exponent
+    if (h >= 0x7c00u) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | h);
+  }
+  if (bexp == 0 && frac == 0) return (uint16_t)sign;
+  uint32_t sh = (uint32_t)(-1 - e);  // >= 14
+  if (sh >= 31) return (uint16_t)sign;
+  uint32_t whole = m >> sh;
+  uint32_t rem = m & ((1u << sh) - 1u);
+  uint32_t half = 1u << (sh - 1);
+  whole += (rem > half) || (rem == half && (whole & 1u));
+  return (uint16_t)(sign | whole);  // whole == 0x400 is the smallest normal
+}
+
+// The f16 encoder of har/crates/har-serve/src/attention.rs:45-76, in integer
+// form.  That code takes exp = floor(log2|v|) and rounds the 10-bit
+// mantissa half away from zero, but keeps only `mantissa & 0x3ff`, so a
+// round-up to 1024 drops the carry (value encodes as 2^exp).  For negative
+// normal inputs its (v/2^exp - 1)*1024 is negative and `as u16` saturates
+// to 0; negative subnormals saturate to -0.
+__host__ __device__ inline uint16_t f16_harserve(float v) {
+  uint32_t x = __builtin_bit_cast(uint32_t, v);
+  uint32_t sign = (x >> 16) & 0x8000u;
+  int32_t bexp = (int32_t)((x >> 23) & 0xffu);
+  uint32_t frac = x & 0x7fffffu;
+  if ((x & 0x7fffffffu) == 0) return (uint16_t)sign;
+  if (bexp == 0xff) return frac ? (uint16_t)0x7e00u : (uint16_t)(sign | 0x7c00u);
+  if (bexp == 0) return (uint16_t)sign;  // f32 subnormal: rounds to (+/-)0 units
+  int32_t e = bexp - 127;
+  if (e < -14) {
+    if (sign) return 0x8000u;
+    uint32_t sh = (uint32_t)(-1 - e);  // v * 2^24 = m * 2^-sh, sh >= 14
+    if (sh >= 26) return 0;
+    uint32_t m = frac | 0x800000u;
+    return (uint16_t)((m + (1u << (sh - 1))) >> sh);
+  }
+  if (e > 15) return (uint16_t)(sign | 0x7c00u);
+  uint32_t mant = sign ? 0u : ((frac + 0x1000u) >> 13);
+  return (uint16_t)(sign | ((uint32_t)(e + 15) << 10) | (mant & 0x3ffu));
+}
+
+// binary16 bits -> f32 (exact), as r4kv/src/f16.rs:4-25 and q4k.rs:22-50.
+__device__ inline float f16_bits_to_f32(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ inline float bf16_bits_to_f32(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+__device__ inline uint16_t f32_to_bf16_rtne(float v) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Rust `roundf(x) as i32` then clamp to [-127, 127] (NaN -> 0).
+__device__ inline int32_t q8_code(float r) {
+  if (r != r) return 0;
+  r = fminf(fmaxf(r, -127.0f), 127.0f);
+  return (int32_t)r;
+}
+
+}  // namespace rkv

@@ -1,0 +1,80 @@
+// rkv_launch.h -- internal launcher interface between the C-ABI runtime
+// (rkv_runtime.cpp) and the gfx950 kernels (rkv_append.hip, rkv_decode.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rkv_device.h"
+
+namespace rkv {
+
+struct AppendLaunch {
+  Geo g;
+  uint8_t *pages;
+  const int32_t *bt;
+  int32_t bt_stride;
+  int32_t n_seqs;
+  int32_t n_rows;
+  const int32_t *seq_ids;
+  const int32_t *positions;
+  const void *k_src;
+  const void *v_src;
+  int32_t src_bf16;
+  int32_t rule;
+  int32_t *fault;
+};
+hipError_t launch_append(const AppendLaunch &a, hipStream_t s);
+
+// gather: pages -> reference rows; import: reference rows -> pages
+hipError_t launch_gather(const Geo &g, const uint8_t *pages, const int32_t *bt, int32_t len,
+                         int32_t kind, uint8_t *rows, int32_t *fault, hipStream_t s);
+hipError_t launch_import(const Geo &g, uint8_t *pages, const int32_t *bt, int32_t len,
+                         int32_t kind, const uint8_t *rows, int32_t *fault, hipStream_t s);
+hipError_t launch_f32_to_f16(const float *in, uint16_t *out, int64_t n, int32_t rule,
+                             hipStream_t s);
+
+struct DecodeLaunch {
+  Geo g;
+  const uint8_t *pages;
+  const int32_t *bt;
+  int32_t bt_stride;
+  const int32_t *seq_lens;
+  int32_t n_seqs;
+  const int32_t *seq_ids;
+  int32_t batch;
+  const void *q;
+  int32_t q_bf16;
+  int32_t q_len;
+  int32_t q_heads;
+  float scale_log2;  // softmax scale * log2(e)
+  int32_t part_tokens;
+  int32_t n_parts;
+  // direct output (ws_o == nullptr) ...
+  void *out;
+  int32_t out_bf16;
+  // ... or split-K partials [batch][q_len*q_heads][n_parts][2 | head_dim]
+  float *ws_ml;
+  float *ws_o;
+  int32_t *fault;
+};
+// rows per kv head = q_len * q_heads / kv_heads must be <= 32
+hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s);
+
+struct CombineLaunch {
+  const float *ml;
+  const float *o;
+  int32_t batch;
+  int32_t rows;
+  int32_t n_parts;
+  int32_t head_dim;
+  const int32_t *seq_ids;
+  const int32_t *seq_lens;
+  int32_t n_seqs;
+  int32_t part_tokens;
+  void *out;
+  int32_t out_bf16;
+};
+hipError_t launch_combine(const CombineLaunch &c, hipStream_t s);
+
+}  // namespace rkv

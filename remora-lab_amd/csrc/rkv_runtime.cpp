@@ -1,0 +1,814 @@
+// rkv_runtime.cpp -- host side of the C ABI in include/rkv.h: errors,
+// device context, page allocator + block tables, pool, argument checking
+// and kernel dispatch.  No entry point computes on the CPU: every data
+// operation is a HIP kernel, and a missing device is an error.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/rkv.h"
+#include "rkv_launch.h"
+
+using rkv::Geo;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+// Mirrors HarError{operation, message} (har-vulkan/src/lib.rs:19-56): the
+// status says what kind of failure, the message says where and why.
+rkv_status fail(rkv_status code, const char *op, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = std::string(op) + ": " + buf;
+  return code;
+}
+
+rkv_status hip_fail(const char *op, hipError_t e) {
+  return fail(RKV_ERR_DEVICE, op, "%s (%s)", hipGetErrorString(e), hipGetErrorName(e));
+}
+
+uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ULL;
+  uint64_t z = x;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebULL;
+  return z ^ (z >> 31);
+}
+
+bool pow2(int32_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+rkv_status check_geometry(const rkv_kv_geometry *g, const char *op) {
+  if (!g) return fail(RKV_ERR_INVALID_ARG, op, "geometry is NULL");
+  if (g->kv_heads < 1 || g->kv_heads > 64)
+    return fail(RKV_ERR_INVALID_ARG, op, "kv_heads=%d outside [1, 64]", g->kv_heads);
+  if (g->head_dim != 128 && g->head_dim != 256)
+    return fail(RKV_ERR_UNSUPPORTED, op, "head_dim=%d (built: 128, 256)", g->head_dim);
+  if (!pow2(g->page_tokens) || g->page_tokens < 16 || g->page_tokens > 256)
+    return fail(RKV_ERR_UNSUPPORTED, op, "page_tokens=%d (built: 16, 32, 64, 128, 256)",
+                g->page_tokens);
+  if (g->num_pages < 1) return fail(RKV_ERR_INVALID_ARG, op, "num_pages=%d", g->num_pages);
+  return RKV_OK;
+}
+
+Geo to_geo(const rkv_kv_geometry *g) {
+  return Geo{g->kv_heads, g->head_dim, g->page_tokens, g->num_pages};
+}
+
+hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// context
+// ---------------------------------------------------------------------------
+struct rkv_ctx {
+  int32_t device = 0;
+  int32_t *d_fault = nullptr;  // device fault word (rkv::FAULT_* bits)
+};
+
+namespace {
+// Make ctx's device current for the calling thread.
+rkv_status use_device(rkv_ctx *ctx, const char *op) {
+  if (!ctx) return fail(RKV_ERR_INVALID_ARG, op, "ctx is NULL");
+  hipError_t e = hipSetDevice(ctx->device);
+  if (e != hipSuccess) return hip_fail(op, e);
+  return RKV_OK;
+}
+}  // namespace
+
+extern "C" {
+
+const char *rkv_last_error(void) { return g_last_error.c_str(); }
+const char *rkv_version(void) { return "rkv 0.1 (gfx950)"; }
+
+rkv_status rkv_ctx_create(int32_t device, rkv_ctx **out) {
+  const char *op = "rkv_ctx_create";
+  if (!out) return fail(RKV_ERR_INVALID_ARG, op, "out is NULL");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0)
+    return fail(RKV_ERR_DEVICE, op, "no HIP device (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n) return fail(RKV_ERR_INVALID_ARG, op, "device %d of %d", device, n);
+  if ((e = hipSetDevice(device)) != hipSuccess) return hip_fail(op, e);
+  hipDeviceProp_t prop;
+  if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return hip_fail(op, e);
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(RKV_ERR_UNSUPPORTED, op, "device %d is %s; kernels are built for gfx950", device,
+                prop.gcnArchName);
+  rkv_ctx *c = new rkv_ctx;
+  c->device = device;
+  if ((e = hipMalloc(&c->d_fault, sizeof(int32_t))) != hipSuccess) {
+    delete c;
+    return hip_fail(op, e);
+  }
+  if ((e = hipMemset(c->d_fault, 0, sizeof(int32_t))) != hipSuccess) {
+    (void)hipFree(c->d_fault);
+    delete c;
+    return hip_fail(op, e);
+  }
+  *out = c;
+  return RKV_OK;
+}
+
+rkv_status rkv_ctx_destroy(rkv_ctx *ctx) {
+  if (!ctx) return RKV_OK;
+  (void)hipSetDevice(ctx->device);
+  (void)hipFree(ctx->d_fault);
+  delete ctx;
+  return RKV_OK;
+}
+
+rkv_status rkv_ctx_sync(rkv_ctx *ctx, void *stream) {
+  const char *op = "rkv_ctx_sync";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  hipError_t e = hipStreamSynchronize(as_stream(stream));
+  if (e != hipSuccess) return hip_fail(op, e);
+  int32_t fault = 0;
+  if ((e = hipMemcpy(&fault, ctx->d_fault, sizeof fault, hipMemcpyDeviceToHost)) != hipSuccess)
+    return hip_fail(op, e);
+  if (fault) {
+    if ((e = hipMemset(ctx->d_fault, 0, sizeof(int32_t))) != hipSuccess) return hip_fail(op, e);
+    return fail(RKV_ERR_BAD_BLOCK_TABLE, op,
+                "device reported fault bits 0x%x (1: page id outside the pool, 2: position "
+                "beyond the block-table row, 4: sequence id outside the table)",
+                fault);
+  }
+  return RKV_OK;
+}
+
+// ---------------------------------------------------------------------------
+// geometry
+// ---------------------------------------------------------------------------
+rkv_status rkv_geometry_check(const rkv_kv_geometry *g) {
+  return check_geometry(g, "rkv_geometry_check");
+}
+size_t rkv_page_bytes(const rkv_kv_geometry *g) {
+  if (!g || check_geometry(g, "rkv_page_bytes") != RKV_OK) return 0;
+  return (size_t)rkv::page_bytes(to_geo(g));
+}
+size_t rkv_row_bytes(int32_t head_dim) {
+  return head_dim > 0 && head_dim % 32 == 0 ? (size_t)head_dim / 32 * 34 : 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// page allocator
+// ---------------------------------------------------------------------------
+struct rkv_alloc {
+  rkv_alloc_desc d{};
+  std::vector<int32_t> free_list;  // top of the stack = back
+  std::vector<int32_t> tables;     // [max_seqs][max_pages_per_seq], -1 = none
+  std::vector<int32_t> lens;       // [max_seqs]
+  std::vector<int32_t> held;       // pages held per sequence
+  std::vector<uint8_t> dirty;      // table row or length changed since last upload
+};
+
+namespace {
+rkv_status check_seq(const rkv_alloc *a, int32_t seq, const char *op) {
+  if (!a) return fail(RKV_ERR_INVALID_ARG, op, "allocator is NULL");
+  if (seq < 0 || seq >= a->d.max_seqs)
+    return fail(RKV_ERR_INVALID_ARG, op, "seq %d outside [0, %d)", seq, a->d.max_seqs);
+  return RKV_OK;
+}
+int32_t pages_for(const rkv_alloc *a, int64_t len) {
+  return (int32_t)((len + a->d.page_tokens - 1) / a->d.page_tokens);
+}
+}  // namespace
+
+extern "C" {
+
+rkv_status rkv_alloc_create(const rkv_alloc_desc *desc, rkv_alloc **out) {
+  const char *op = "rkv_alloc_create";
+  if (!desc || !out) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  *out = nullptr;
+  if (desc->num_pages < 1 || desc->max_seqs < 1 || desc->max_pages_per_seq < 1)
+    return fail(RKV_ERR_INVALID_ARG, op, "num_pages=%d max_seqs=%d max_pages_per_seq=%d",
+                desc->num_pages, desc->max_seqs, desc->max_pages_per_seq);
+  if (!pow2(desc->page_tokens) || desc->page_tokens < 16 || desc->page_tokens > 256)
+    return fail(RKV_ERR_UNSUPPORTED, op, "page_tokens=%d", desc->page_tokens);
+  if ((int64_t)desc->max_seqs * desc->max_pages_per_seq > (int64_t)1 << 31)
+    return fail(RKV_ERR_INVALID_ARG, op, "block table too large");
+  rkv_alloc *a = new rkv_alloc;
+  a->d = *desc;
+  // Seeded Fisher-Yates permutation of [0, num_pages): pages are handed out
+  // from the back, so the first sequence gets a shuffled page run.
+  a->free_list.resize(desc->num_pages);
+  for (int32_t i = 0; i < desc->num_pages; ++i) a->free_list[i] = i;
+  uint64_t st = desc->free_list_seed;
+  for (int32_t i = desc->num_pages - 1; i > 0; --i) {
+    st = splitmix64(st);
+    int32_t j = (int32_t)(st % (uint64_t)(i + 1));
+    std::swap(a->free_list[i], a->free_list[j]);
+  }
+  a->tables.assign((size_t)desc->max_seqs * desc->max_pages_per_seq, -1);
+  a->lens.assign(desc->max_seqs, 0);
+  a->held.assign(desc->max_seqs, 0);
+  a->dirty.assign(desc->max_seqs, 1);
+  *out = a;
+  return RKV_OK;
+}
+
+rkv_status rkv_alloc_destroy(rkv_alloc *a) {
+  delete a;
+  return RKV_OK;
+}
+
+rkv_status rkv_seq_reserve(rkv_alloc *a, int32_t seq, int32_t new_len) {
+  const char *op = "rkv_seq_reserve";
+  if (rkv_status s = check_seq(a, seq, op)) return s;
+  if (new_len < a->lens[seq])
+    return fail(RKV_ERR_INVALID_ARG, op, "seq %d: new_len %d < length %d (use rkv_seq_truncate)",
+                seq, new_len, a->lens[seq]);
+  const int32_t need = pages_for(a, new_len);
+  if (need > a->d.max_pages_per_seq)
+    return fail(RKV_ERR_CAPACITY, op, "seq %d: %d tokens need %d pages > max_pages_per_seq %d",
+                seq, new_len, need, a->d.max_pages_per_seq);
+  const int32_t extra = need - a->held[seq];
+  if (extra > (int32_t)a->free_list.size())
+    return fail(RKV_ERR_OUT_OF_PAGES, op, "seq %d needs %d more pages, %zu free", seq, extra,
+                a->free_list.size());
+  int32_t *row = &a->tables[(size_t)seq * a->d.max_pages_per_seq];
+  for (int32_t i = a->held[seq]; i < need; ++i) {
+    row[i] = a->free_list.back();
+    a->free_list.pop_back();
+  }
+  a->held[seq] = std::max(a->held[seq], need);
+  a->lens[seq] = new_len;
+  a->dirty[seq] = 1;
+  return RKV_OK;
+}
+
+rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len) {
+  const char *op = "rkv_seq_truncate";
+  if (rkv_status s = check_seq(a, seq, op)) return s;
+  if (new_len < 0 || new_len > a->lens[seq])
+    return fail(RKV_ERR_INVALID_ARG, op, "seq %d: new_len %d outside [0, %d]", seq, new_len,
+                a->lens[seq]);
+  const int32_t keep = pages_for(a, new_len);
+  int32_t *row = &a->tables[(size_t)seq * a->d.max_pages_per_seq];
+  // return pages last-first so a re-grow gets the same pages back
+  for (int32_t i = a->held[seq] - 1; i >= keep; --i) {
+    a->free_list.push_back(row[i]);
+    row[i] = -1;
+  }
+  a->held[seq] = std::min(a->held[seq], keep);
+  a->lens[seq] = new_len;
+  a->dirty[seq] = 1;
+  return RKV_OK;
+}
+
+rkv_status rkv_seq_free(rkv_alloc *a, int32_t seq) { return rkv_seq_truncate(a, seq, 0); }
+
+rkv_status rkv_seq_len(const rkv_alloc *a, int32_t seq, int32_t *len) {
+  const char *op = "rkv_seq_len";
+  if (rkv_status s = check_seq(a, seq, op)) return s;
+  if (!len) return fail(RKV_ERR_INVALID_ARG, op, "len is NULL");
+  *len = a->lens[seq];
+  return RKV_OK;
+}
+
+rkv_status rkv_block_table_get(const rkv_alloc *a, int32_t seq, int32_t *out, int32_t cap,
+                               int32_t *n) {
+  const char *op = "rkv_block_table_get";
+  if (rkv_status s = check_seq(a, seq, op)) return s;
+  if (!n) return fail(RKV_ERR_INVALID_ARG, op, "n is NULL");
+  *n = a->held[seq];
+  if (cap < a->held[seq])
+    return fail(RKV_ERR_INVALID_ARG, op, "cap %d < %d pages", cap, a->held[seq]);
+  if (a->held[seq] > 0 && !out) return fail(RKV_ERR_INVALID_ARG, op, "out is NULL");
+  std::memcpy(out, &a->tables[(size_t)seq * a->d.max_pages_per_seq],
+              sizeof(int32_t) * (size_t)a->held[seq]);
+  return RKV_OK;
+}
+
+rkv_status rkv_alloc_free_pages(const rkv_alloc *a, int32_t *n) {
+  if (!a || !n) return fail(RKV_ERR_INVALID_ARG, "rkv_alloc_free_pages", "NULL argument");
+  *n = (int32_t)a->free_list.size();
+  return RKV_OK;
+}
+
+rkv_status rkv_alloc_export(const rkv_alloc *a, int32_t *tables, int32_t *lens) {
+  if (!a || !tables || !lens) return fail(RKV_ERR_INVALID_ARG, "rkv_alloc_export", "NULL argument");
+  std::memcpy(tables, a->tables.data(), sizeof(int32_t) * a->tables.size());
+  std::memcpy(lens, a->lens.data(), sizeof(int32_t) * a->lens.size());
+  return RKV_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// kernel-level operations
+// ---------------------------------------------------------------------------
+namespace {
+
+int32_t auto_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *a) {
+  // Aim for >= ~2048 work units over the 256 CUs, in tiles of 32 tokens,
+  // never more than 64 pages per partition (the kernel keeps one page id
+  // per lane).
+  const int64_t max_len = std::max<int64_t>(a->max_seq_len, 1);
+  const int64_t units_per_part = (int64_t)a->batch * g->kv_heads;
+  int64_t parts = (2048 + units_per_part - 1) / std::max<int64_t>(units_per_part, 1);
+  int64_t pt = (max_len + parts - 1) / parts;
+  const int64_t unit = std::max<int32_t>(32, g->page_tokens);
+  pt = std::max<int64_t>(pt, 256);
+  pt = (pt + unit - 1) / unit * unit;
+  pt = std::min<int64_t>(pt, 64 * (int64_t)g->page_tokens);
+  return (int32_t)pt;
+}
+
+rkv_status check_decode(const rkv_kv_geometry *g, const rkv_decode_args *a, const char *op) {
+  if (rkv_status s = check_geometry(g, op)) return s;
+  if (!a) return fail(RKV_ERR_INVALID_ARG, op, "args is NULL");
+  if (a->batch < 0) return fail(RKV_ERR_INVALID_ARG, op, "batch=%d", a->batch);
+  if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "q_heads=%d is not a multiple of kv_heads=%d",
+                a->q_heads, g->kv_heads);
+  if (a->q_len < 1 || a->q_len > 4) return fail(RKV_ERR_UNSUPPORTED, op, "q_len=%d (1..4)", a->q_len);
+  const int32_t R = a->q_len * (a->q_heads / g->kv_heads);
+  if (R > 32)
+    return fail(RKV_ERR_UNSUPPORTED, op, "q_len*q_heads/kv_heads=%d rows per kv head (<= 32)", R);
+  if (a->q_dtype != RKV_F32 && a->q_dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, op, "q_dtype=%d", a->q_dtype);
+  if (a->out_dtype != RKV_F32 && a->out_dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, op, "out_dtype=%d", a->out_dtype);
+  if (!(std::isfinite(a->scale))) return fail(RKV_ERR_INVALID_ARG, op, "scale is not finite");
+  // partitions start on page (and 32-token tile) boundaries and span at most
+  // 64 pages: the kernel keeps one page id per lane
+  const int32_t unit = std::max<int32_t>(32, g->page_tokens);
+  if (a->partition_tokens < 0 || a->partition_tokens % unit != 0 ||
+      a->partition_tokens > 64 * g->page_tokens)
+    return fail(RKV_ERR_INVALID_ARG, op,
+                "partition_tokens=%d must be a multiple of %d and <= 64*page_tokens (%d)",
+                a->partition_tokens, unit, 64 * g->page_tokens);
+  if (a->max_seq_len < 0) return fail(RKV_ERR_INVALID_ARG, op, "max_seq_len=%d", a->max_seq_len);
+  if (a->batch > 0 && (!a->seq_ids || !a->q || !a->out))
+    return fail(RKV_ERR_INVALID_ARG, op, "NULL seq_ids/q/out");
+  if (a->batch > 65535) return fail(RKV_ERR_INVALID_ARG, op, "batch=%d > 65535", a->batch);
+  return RKV_OK;
+}
+
+int32_t parts_of(const rkv_decode_args *a, int32_t pt) {
+  return std::max<int32_t>(1, (a->max_seq_len + pt - 1) / pt);
+}
+
+size_t ws_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a, int32_t pt) {
+  const int32_t np = parts_of(a, pt);
+  if (np == 1) return 0;
+  const size_t rows = (size_t)a->batch * a->q_len * a->q_heads * np;
+  return rows * (2 + (size_t)g->head_dim) * sizeof(float);
+}
+
+rkv::DecodeLaunch make_decode(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                              const int32_t *bt, int32_t bt_stride, const int32_t *seq_lens,
+                              int32_t n_seqs, const rkv_decode_args *a, int32_t pt) {
+  rkv::DecodeLaunch d{};
+  d.g = to_geo(g);
+  d.pages = static_cast<const uint8_t *>(pages);
+  d.bt = bt;
+  d.bt_stride = bt_stride;
+  d.seq_lens = seq_lens;
+  d.n_seqs = n_seqs;
+  d.seq_ids = a->seq_ids;
+  d.batch = a->batch;
+  d.q = a->q;
+  d.q_bf16 = a->q_dtype == RKV_BF16;
+  d.q_len = a->q_len;
+  d.q_heads = a->q_heads;
+  d.scale_log2 = a->scale * 1.4426950408889634f;
+  d.part_tokens = pt;
+  d.n_parts = parts_of(a, pt);
+  d.out = a->out;
+  d.out_bf16 = a->out_dtype == RKV_BF16;
+  d.fault = ctx->d_fault;
+  return d;
+}
+
+rkv_status check_tables(const void *pages, const int32_t *bt, int32_t bt_stride,
+                        int32_t n_seqs, const char *op) {
+  if (!pages || !bt) return fail(RKV_ERR_INVALID_ARG, op, "NULL pages/block_tables");
+  if (bt_stride < 1 || n_seqs < 1)
+    return fail(RKV_ERR_INVALID_ARG, op, "bt_stride=%d n_seqs=%d", bt_stride, n_seqs);
+  return RKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
+                         const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
+                         const rkv_append_args *args, void *stream) {
+  const char *op = "rkv_append_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_geometry(g, op)) return s;
+  if (rkv_status s = check_tables(pages, block_tables, bt_stride, n_seqs, op)) return s;
+  if (!args) return fail(RKV_ERR_INVALID_ARG, op, "args is NULL");
+  if (args->n_rows < 0) return fail(RKV_ERR_INVALID_ARG, op, "n_rows=%d", args->n_rows);
+  if (args->src_dtype != RKV_F32 && args->src_dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, op, "src_dtype=%d", args->src_dtype);
+  if (args->rule != RKV_Q8_CANONICAL && args->rule != RKV_Q8_HARSERVE)
+    return fail(RKV_ERR_INVALID_ARG, op, "rule=%d", args->rule);
+  if (args->n_rows == 0) return RKV_OK;
+  if (!args->seq_ids || !args->positions || !args->k_src || !args->v_src)
+    return fail(RKV_ERR_INVALID_ARG, op, "NULL seq_ids/positions/k_src/v_src");
+  rkv::AppendLaunch a{};
+  a.g = to_geo(g);
+  a.pages = static_cast<uint8_t *>(pages);
+  a.bt = block_tables;
+  a.bt_stride = bt_stride;
+  a.n_seqs = n_seqs;
+  a.n_rows = args->n_rows;
+  a.seq_ids = args->seq_ids;
+  a.positions = args->positions;
+  a.k_src = args->k_src;
+  a.v_src = args->v_src;
+  a.src_bf16 = args->src_dtype == RKV_BF16;
+  a.rule = args->rule;
+  a.fault = ctx->d_fault;
+  hipError_t e = rkv::launch_append(a, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+int32_t rkv_decode_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *a) {
+  if (!g || !a) return 0;
+  return a->partition_tokens > 0 ? a->partition_tokens : auto_partition_tokens(g, a);
+}
+
+size_t rkv_decode_workspace_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a) {
+  if (!g || !a || check_geometry(g, "rkv_decode_workspace_bytes") != RKV_OK) return 0;
+  return ws_bytes(g, a, rkv_decode_partition_tokens(g, a));
+}
+
+rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                         const int32_t *block_tables, int32_t bt_stride,
+                         const int32_t *seq_lens, int32_t n_seqs, const rkv_decode_args *a,
+                         void *stream) {
+  const char *op = "rkv_decode_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_decode(g, a, op)) return s;
+  if (rkv_status s = check_tables(pages, block_tables, bt_stride, n_seqs, op)) return s;
+  if (!seq_lens) return fail(RKV_ERR_INVALID_ARG, op, "seq_lens is NULL");
+  if (a->batch == 0) return RKV_OK;
+  const int32_t pt = rkv_decode_partition_tokens(g, a);
+  rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pt);
+  const size_t need = ws_bytes(g, a, pt);
+  if (d.n_parts > 1) {
+    if (!a->workspace || a->workspace_bytes < need)
+      return fail(RKV_ERR_INVALID_ARG, op, "workspace %zu bytes < %zu needed for %d partitions",
+                  a->workspace_bytes, need, d.n_parts);
+    const size_t rows = (size_t)a->batch * a->q_len * a->q_heads * d.n_parts;
+    d.ws_ml = static_cast<float *>(a->workspace);
+    d.ws_o = d.ws_ml + 2 * rows;
+  }
+  hipError_t e = rkv::launch_decode(d, as_stream(stream));
+  if (e != hipSuccess) return hip_fail(op, e);
+  if (d.n_parts > 1) {
+    rkv::CombineLaunch c{};
+    c.ml = d.ws_ml;
+    c.o = d.ws_o;
+    c.batch = a->batch;
+    c.rows = a->q_len * a->q_heads;
+    c.n_parts = d.n_parts;
+    c.head_dim = g->head_dim;
+    c.seq_ids = a->seq_ids;
+    c.seq_lens = seq_lens;
+    c.n_seqs = n_seqs;
+    c.part_tokens = pt;
+    c.out = a->out;
+    c.out_bf16 = d.out_bf16;
+    e = rkv::launch_combine(c, as_stream(stream));
+    if (e != hipSuccess) return hip_fail(op, e);
+  }
+  return RKV_OK;
+}
+
+rkv_status rkv_decode_q8_partials(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                                  const int32_t *block_tables, int32_t bt_stride,
+                                  const int32_t *seq_lens, int32_t n_seqs,
+                                  const rkv_decode_args *a, float *ml, float *o, void *stream) {
+  const char *op = "rkv_decode_q8_partials";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_decode(g, a, op)) return s;
+  if (rkv_status s = check_tables(pages, block_tables, bt_stride, n_seqs, op)) return s;
+  if (!seq_lens || !ml || !o) return fail(RKV_ERR_INVALID_ARG, op, "NULL seq_lens/ml/o");
+  if (a->batch == 0) return RKV_OK;
+  const int32_t pt = rkv_decode_partition_tokens(g, a);
+  rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pt);
+  d.ws_ml = ml;  // non-null workspace: the kernel writes partials, even for one partition
+  d.ws_o = o;
+  d.out = nullptr;
+  hipError_t e = rkv::launch_decode(d, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+rkv_status rkv_splitk_combine(rkv_ctx *ctx, const float *ml, const float *o, int32_t batch,
+                              int32_t rows, int32_t n_parts, int32_t head_dim,
+                              const int32_t *seq_ids, const int32_t *seq_lens, int32_t n_seqs,
+                              int32_t partition_tokens, void *out, int32_t out_dtype,
+                              void *stream) {
+  const char *op = "rkv_splitk_combine";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (!ml || !o || !seq_ids || !seq_lens || !out)
+    return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  if (batch < 0 || rows < 1 || n_parts < 1 || partition_tokens < 1)
+    return fail(RKV_ERR_INVALID_ARG, op, "batch=%d rows=%d n_parts=%d partition_tokens=%d", batch,
+                rows, n_parts, partition_tokens);
+  if (head_dim < 1 || head_dim > 256)
+    return fail(RKV_ERR_UNSUPPORTED, op, "head_dim=%d (<= 256)", head_dim);
+  if (out_dtype != RKV_F32 && out_dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, op, "out_dtype=%d", out_dtype);
+  if (n_seqs < 1) return fail(RKV_ERR_INVALID_ARG, op, "n_seqs=%d", n_seqs);
+  rkv::CombineLaunch c{ml, o, batch, rows, n_parts, head_dim, seq_ids, seq_lens, n_seqs,
+                       partition_tokens, out, out_dtype == RKV_BF16};
+  hipError_t e = rkv::launch_combine(c, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+rkv_status rkv_gather_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                         const int32_t *block_table, int32_t len, int32_t kind, uint8_t *out,
+                         void *stream) {
+  const char *op = "rkv_gather_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_geometry(g, op)) return s;
+  if (kind != RKV_K && kind != RKV_V) return fail(RKV_ERR_INVALID_ARG, op, "kind=%d", kind);
+  if (len < 0) return fail(RKV_ERR_INVALID_ARG, op, "len=%d", len);
+  if (len == 0) return RKV_OK;
+  if (!pages || !block_table || !out) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  hipError_t e = rkv::launch_gather(to_geo(g), static_cast<const uint8_t *>(pages), block_table,
+                                    len, kind, out, ctx->d_fault, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+rkv_status rkv_import_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
+                         const int32_t *block_table, int32_t len, int32_t kind,
+                         const uint8_t *rows, void *stream) {
+  const char *op = "rkv_import_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_geometry(g, op)) return s;
+  if (kind != RKV_K && kind != RKV_V) return fail(RKV_ERR_INVALID_ARG, op, "kind=%d", kind);
+  if (len < 0) return fail(RKV_ERR_INVALID_ARG, op, "len=%d", len);
+  if (len == 0) return RKV_OK;
+  if (!pages || !block_table || !rows) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  hipError_t e = rkv::launch_import(to_geo(g), static_cast<uint8_t *>(pages), block_table, len,
+                                    kind, rows, ctx->d_fault, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+rkv_status rkv_f32_to_f16(rkv_ctx *ctx, const float *in, uint16_t *out, int64_t n, int32_t rule,
+                          void *stream) {
+  const char *op = "rkv_f32_to_f16";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (n < 0 || (n > 0 && (!in || !out))) return fail(RKV_ERR_INVALID_ARG, op, "bad buffer");
+  if (rule != RKV_Q8_CANONICAL && rule != RKV_Q8_HARSERVE)
+    return fail(RKV_ERR_INVALID_ARG, op, "rule=%d", rule);
+  hipError_t e = rkv::launch_f32_to_f16(in, out, n, rule, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+// ---------------------------------------------------------------------------
+// flash_decode_q8.comp drop-in: contiguous rows -> scratch pages -> decode
+// ---------------------------------------------------------------------------
+// Scratch layout: [pages][block table int32 ceil(seq_len/64)][seq_len int32]
+// [seq_id int32], all 256-byte aligned.
+namespace {
+struct FdScratch {
+  rkv_kv_geometry g;
+  size_t pages_off, bt_off, len_off, sid_off, ws_off, total;
+  int32_t n_pages;
+};
+FdScratch fd_scratch(const rkv_flash_decode_params *p) {
+  FdScratch s{};
+  s.g.kv_heads = p->kv_heads;
+  s.g.head_dim = p->head_dim;
+  s.g.page_tokens = 64;
+  s.n_pages = std::max(1, (p->seq_len + 63) / 64);
+  s.g.num_pages = s.n_pages;
+  auto up = [](size_t v) { return (v + 255) / 256 * 256; };
+  s.pages_off = 0;
+  s.bt_off = up(s.pages_off + (size_t)s.n_pages * rkv::page_bytes(to_geo(&s.g)));
+  s.len_off = up(s.bt_off + sizeof(int32_t) * s.n_pages);
+  s.sid_off = up(s.len_off + sizeof(int32_t));
+  s.ws_off = up(s.sid_off + sizeof(int32_t));
+  s.total = s.ws_off;
+  return s;
+}
+rkv_decode_args fd_args(const rkv_flash_decode_params *p, const FdScratch &s, uint8_t *base,
+                        const float *query, float *out) {
+  rkv_decode_args a{};
+  a.batch = 1;
+  a.seq_ids = reinterpret_cast<const int32_t *>(base + s.sid_off);
+  a.q = query;
+  a.q_dtype = RKV_F32;
+  a.q_len = 1;
+  a.q_heads = p->q_heads;
+  a.scale = 1.0f;  // flash_decode_q8.comp applies no softmax scale
+  a.out = out;
+  a.out_dtype = RKV_F32;
+  a.max_seq_len = p->seq_len;
+  // one partition covers the sequence when it fits 64 pages; else split
+  a.partition_tokens = 0;
+  return a;
+}
+}  // namespace
+
+size_t rkv_flash_decode_scratch_bytes(const rkv_flash_decode_params *p) {
+  if (!p || p->seq_len < 0 || p->kv_heads < 1) return 0;
+  FdScratch s = fd_scratch(p);
+  rkv_decode_args a = fd_args(p, s, nullptr, nullptr, nullptr);
+  return s.total + rkv_decode_workspace_bytes(&s.g, &a);
+}
+
+rkv_status rkv_flash_decode_q8(rkv_ctx *ctx, const rkv_flash_decode_params *p,
+                               const uint32_t *k_words, const uint32_t *v_words,
+                               const float *query, float *out, void *scratch, void *stream) {
+  const char *op = "rkv_flash_decode_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (!p || !query || !out || !scratch) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  // smoke :47-51 asserts the GQA divisibility
+  if (p->kv_heads < 1 || p->q_heads % p->kv_heads != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "GQA requires q_heads %% kv_heads == 0 (%d, %d)",
+                p->q_heads, p->kv_heads);
+  if (p->seq_len < 0) return fail(RKV_ERR_INVALID_ARG, op, "seq_len=%d", p->seq_len);
+  if (p->seq_len > 0 && (!k_words || !v_words)) return fail(RKV_ERR_INVALID_ARG, op, "NULL K/V");
+  FdScratch s = fd_scratch(p);
+  if (rkv_status st = check_geometry(&s.g, op)) return st;
+  uint8_t *base = static_cast<uint8_t *>(scratch);
+  hipStream_t hs = as_stream(stream);
+  // identity block table, length and sequence id, written by a tiny upload
+  std::vector<int32_t> bt(s.n_pages);
+  for (int32_t i = 0; i < s.n_pages; ++i) bt[i] = i;
+  const int32_t meta[2] = {p->seq_len, 0};
+  hipError_t e;
+  if ((e = hipMemcpyAsync(base + s.bt_off, bt.data(), sizeof(int32_t) * s.n_pages,
+                          hipMemcpyHostToDevice, hs)) != hipSuccess)
+    return hip_fail(op, e);
+  if ((e = hipMemcpyAsync(base + s.len_off, &meta[0], sizeof(int32_t), hipMemcpyHostToDevice, hs)) !=
+      hipSuccess)
+    return hip_fail(op, e);
+  if ((e = hipMemcpyAsync(base + s.sid_off, &meta[1], sizeof(int32_t), hipMemcpyHostToDevice, hs)) !=
+      hipSuccess)
+    return hip_fail(op, e);
+  // the host copies above come from stack/vector memory: finish them first
+  if ((e = hipStreamSynchronize(hs)) != hipSuccess) return hip_fail(op, e);
+  const int32_t *dbt = reinterpret_cast<const int32_t *>(base + s.bt_off);
+  if (p->seq_len > 0) {
+    if (rkv_status st = rkv_import_q8(ctx, &s.g, base + s.pages_off, dbt, p->seq_len, RKV_K,
+                                      reinterpret_cast<const uint8_t *>(k_words), stream))
+      return st;
+    if (rkv_status st = rkv_import_q8(ctx, &s.g, base + s.pages_off, dbt, p->seq_len, RKV_V,
+                                      reinterpret_cast<const uint8_t *>(v_words), stream))
+      return st;
+  }
+  rkv_decode_args a = fd_args(p, s, base, query, out);
+  a.workspace = base + s.ws_off;
+  a.workspace_bytes = rkv_decode_workspace_bytes(&s.g, &a);
+  return rkv_decode_q8(ctx, &s.g, base + s.pages_off, dbt, s.n_pages,
+                       reinterpret_cast<const int32_t *>(base + s.len_off), 1, &a, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// pool
+// ---------------------------------------------------------------------------
+struct rkv_pool {
+  rkv_ctx *ctx = nullptr;
+  rkv_pool_desc d{};
+  rkv_kv_geometry g{};
+  rkv_alloc *alloc = nullptr;
+  uint8_t *pages = nullptr;  // layers * num_pages * page_bytes
+  size_t layer_bytes = 0;
+  int32_t *d_tables = nullptr;
+  int32_t *d_lens = nullptr;
+};
+
+extern "C" {
+
+rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **out) {
+  const char *op = "rkv_pool_create";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (!desc || !out) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  *out = nullptr;
+  if (desc->layers < 1) return fail(RKV_ERR_INVALID_ARG, op, "layers=%d", desc->layers);
+  rkv_kv_geometry g{desc->kv_heads, desc->head_dim, desc->page_tokens, desc->num_pages};
+  if (rkv_status s = check_geometry(&g, op)) return s;
+  rkv_alloc_desc ad{desc->num_pages, desc->page_tokens, desc->max_seqs, desc->max_pages_per_seq,
+                    desc->free_list_seed};
+  rkv_pool *p = new rkv_pool;
+  p->ctx = ctx;
+  p->d = *desc;
+  p->g = g;
+  if (rkv_status s = rkv_alloc_create(&ad, &p->alloc)) {
+    delete p;
+    return s;
+  }
+  p->layer_bytes = (size_t)desc->num_pages * rkv::page_bytes(to_geo(&g));
+  hipError_t e;
+  const size_t tbytes = sizeof(int32_t) * (size_t)desc->max_seqs * desc->max_pages_per_seq;
+  if ((e = hipMalloc(&p->pages, p->layer_bytes * desc->layers)) != hipSuccess ||
+      (e = hipMalloc(&p->d_tables, tbytes)) != hipSuccess ||
+      (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess) {
+    rkv_status s = fail(RKV_ERR_DEVICE, op, "hipMalloc of %zu page bytes: %s",
+                        p->layer_bytes * desc->layers, hipGetErrorString(e));
+    rkv_pool_destroy(p);
+    return s;
+  }
+  // zeroed pages: never-written slots hold finite codes and scales
+  if ((e = hipMemset(p->pages, 0, p->layer_bytes * desc->layers)) != hipSuccess) {
+    rkv_pool_destroy(p);
+    return hip_fail(op, e);
+  }
+  if (rkv_status s = rkv_pool_sync_tables(p, nullptr)) {
+    rkv_pool_destroy(p);
+    return s;
+  }
+  *out = p;
+  return RKV_OK;
+}
+
+rkv_status rkv_pool_destroy(rkv_pool *p) {
+  if (!p) return RKV_OK;
+  if (p->ctx) (void)hipSetDevice(p->ctx->device);
+  (void)hipFree(p->pages);
+  (void)hipFree(p->d_tables);
+  (void)hipFree(p->d_lens);
+  rkv_alloc_destroy(p->alloc);
+  delete p;
+  return RKV_OK;
+}
+
+rkv_alloc *rkv_pool_allocator(rkv_pool *p) { return p ? p->alloc : nullptr; }
+
+rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
+  const char *op = "rkv_pool_sync_tables";
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  // Blocking copies of the changed rows: host-side allocator edits happen
+  // between steps, and the copies are ordered after `stream`'s prior work.
+  hipError_t e = hipStreamSynchronize(as_stream(stream));
+  if (e != hipSuccess) return hip_fail(op, e);
+  rkv_alloc *a = p->alloc;
+  const size_t W = (size_t)a->d.max_pages_per_seq;
+  bool lens_dirty = false;
+  for (int32_t s = 0; s < a->d.max_seqs; ++s) {
+    if (!a->dirty[s]) continue;
+    lens_dirty = true;
+    if ((e = hipMemcpy(p->d_tables + s * W, &a->tables[s * W], sizeof(int32_t) * W,
+                       hipMemcpyHostToDevice)) != hipSuccess)
+      return hip_fail(op, e);
+    a->dirty[s] = 0;
+  }
+  if (lens_dirty &&
+      (e = hipMemcpy(p->d_lens, a->lens.data(), sizeof(int32_t) * a->lens.size(),
+                     hipMemcpyHostToDevice)) != hipSuccess)
+    return hip_fail(op, e);
+  return RKV_OK;
+}
+
+void *rkv_pool_layer_pages(rkv_pool *p, int32_t layer) {
+  if (!p || layer < 0 || layer >= p->d.layers) return nullptr;
+  return p->pages + (size_t)layer * p->layer_bytes;
+}
+const int32_t *rkv_pool_block_tables(rkv_pool *p) { return p ? p->d_tables : nullptr; }
+const int32_t *rkv_pool_seq_lens(rkv_pool *p) { return p ? p->d_lens : nullptr; }
+
+rkv_status rkv_pool_append(rkv_pool *p, int32_t layer, const rkv_append_args *args, void *stream) {
+  const char *op = "rkv_pool_append";
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
+  return rkv_append_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
+                       p->d.max_pages_per_seq, p->d.max_seqs, args, stream);
+}
+
+rkv_status rkv_pool_decode(rkv_pool *p, int32_t layer, const rkv_decode_args *args, void *stream) {
+  const char *op = "rkv_pool_decode";
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
+  return rkv_decode_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
+                       p->d.max_pages_per_seq, p->d_lens, p->d.max_seqs, args, stream);
+}
+
+rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind, uint8_t *out,
+                           void *stream) {
+  const char *op = "rkv_pool_gather";
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
+  if (rkv_status s = check_seq(p->alloc, seq, op)) return s;
+  return rkv_gather_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer),
+                       p->d_tables + (size_t)seq * p->d.max_pages_per_seq, p->alloc->lens[seq],
+                       kind, out, stream);
+}
+
+}  // extern "C"

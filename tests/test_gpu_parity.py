@@ -1,0 +1,499 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bars:
+  - page bytes, scales and block-table gathers: bit-exact;
+  - attention outputs: max |gpu - oracle| <= 2e-3 and
+    ||gpu - oracle||_2 / ||oracle||_2 <= 1e-3 over the output tensor.
+The oracle decodes with the reference's chunked loop (attention.rs:169-215)
+using chunk = the kernel's partition length; q is prescaled by `scale` in f32
+(the reference itself applies no scale).
+"""
+import math
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+RTOL = 1e-3
+
+
+def assert_close(got, want, atol=ATOL, rtol=RTOL, what=""):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert got.shape == want.shape
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    err = float(np.max(np.abs(got - want))) if got.size else 0.0
+    den = float(np.linalg.norm(want))
+    rel = float(np.linalg.norm(got - want)) / den if den > 0 else float(np.linalg.norm(got))
+    print(f"[{what}] max_abs={err:.3e} rel={rel:.3e}", flush=True)
+    assert err <= atol, f"{what}: max abs err {err:.3e} > {atol}"
+    assert rel <= rtol, f"{what}: rel err {rel:.3e} > {rtol}"
+
+
+def _torch():
+    import torch
+    return torch
+
+
+class Scene:
+    """A shuffled page pool holding B sequences of the given lengths."""
+
+    def __init__(self, rkv, rko, Hkv, D, PT, lens, seed=0, slack=1.1, outliers=0.0,
+                 src_bf16=False, rule=0, extra_rows=None):
+        torch = _torch()
+        rng = np.random.default_rng(seed)
+        self.Hkv, self.D, self.PT = Hkv, D, PT
+        self.lens = np.asarray(lens, np.int32)
+        B = len(lens)
+        npg = [(int(L) + PT - 1) // PT for L in lens]
+        self.W = max(max(npg), 1)
+        self.num_pages = max(int(math.ceil(sum(npg) * slack)) + 1, 2)
+        perm = rng.permutation(self.num_pages).astype(np.int32)
+        self.bt = np.full((B, self.W), -1, np.int32)
+        o = 0
+        for b in range(B):
+            self.bt[b, :npg[b]] = perm[o:o + npg[b]]
+            o += npg[b]
+        self.g = rkv.geometry(Hkv, D, PT, self.num_pages)
+        self.lay = rko.layout(Hkv, D, PT, self.num_pages)
+        n = int(self.lens.sum())
+        k = rng.standard_normal((n, Hkv, D)).astype(np.float32)
+        v = rng.standard_normal((n, Hkv, D)).astype(np.float32)
+        if outliers:
+            nch = max(1, int(math.ceil(outliers * D)))
+            for h in range(Hkv):
+                ch = rng.choice(D, nch, replace=False)
+                k[:, h, ch] *= 8
+                v[:, h, ch] *= 8
+        if src_bf16:
+            k = rko.bf16_to_f32(rko.f32_to_bf16(k)).reshape(k.shape)
+            v = rko.bf16_to_f32(rko.f32_to_bf16(v)).reshape(v.shape)
+        self.k, self.v = k, v
+        self.seq_ids = np.repeat(np.arange(B, dtype=np.int32), self.lens)
+        self.pos = np.concatenate([np.arange(L, dtype=np.int32) for L in lens]) if n else \
+            np.zeros(0, np.int32)
+        # device
+        dev = "cuda"
+        pb = rkv.page_bytes(self.g)
+        self.pages_d = torch.zeros(self.num_pages * pb, dtype=torch.uint8, device=dev)
+        self.bt_d = torch.from_numpy(self.bt).to(dev)
+        self.lens_d = torch.from_numpy(self.lens).to(dev)
+        if n:
+            sd = torch.from_numpy(self.seq_ids).to(dev)
+            pd = torch.from_numpy(self.pos).to(dev)
+            if src_bf16:
+                kd = torch.from_numpy(k).to(dev).to(torch.bfloat16)
+                vd = torch.from_numpy(v).to(dev).to(torch.bfloat16)
+            else:
+                kd = torch.from_numpy(k).to(dev)
+                vd = torch.from_numpy(v).to(dev)
+            rkv.append_q8(self.ctx_holder[0], self.g, self.pages_d, self.bt_d, sd, pd, kd, vd,
+                          rule=rule)
+        # oracle
+        self.pages = np.zeros(self.num_pages * pb, np.uint8)
+        if n:
+            rko.paged_append(self.lay, self.pages, self.bt, self.seq_ids, self.pos, k, v, rule)
+
+    ctx_holder = [None]
+
+
+@pytest.fixture(autouse=True)
+def _bind_ctx(ctx):
+    Scene.ctx_holder[0] = ctx
+    yield
+
+
+def _run_decode(rkv, ctx, sc, q_np, scale, q_bf16=False, q_len=1, partition_tokens=0,
+                out_bf16=False, seq_ids=None):
+    torch = _torch()
+    B = q_np.shape[0] if seq_ids is None else len(seq_ids)
+    sid = np.arange(B, dtype=np.int32) if seq_ids is None else np.asarray(seq_ids, np.int32)
+    qd = torch.from_numpy(q_np).cuda()
+    if q_bf16:
+        qd = qd.to(torch.bfloat16)
+    out = torch.empty(q_np.shape, dtype=torch.bfloat16 if out_bf16 else torch.float32, device="cuda")
+    sid_d = torch.from_numpy(sid).cuda()
+    a = rkv.decode_args(qd, out, sid_d, scale, int(sc.lens.max()) if len(sc.lens) else 0,
+                        q_len=q_len, partition_tokens=partition_tokens)
+    ws_bytes = rkv.decode_workspace_bytes(sc.g, a)
+    ws = torch.empty(max(ws_bytes, 4), dtype=torch.uint8, device="cuda")
+    a = rkv.decode_args(qd, out, sid_d, scale, int(sc.lens.max()) if len(sc.lens) else 0,
+                        q_len=q_len, partition_tokens=partition_tokens, workspace=ws)
+    pt = rkv.decode_partition_tokens(sc.g, a)
+    rkv.decode_q8(ctx, sc.g, sc.pages_d, sc.bt_d, sc.lens_d, a)
+    ctx.sync()
+    return out.float().cpu().numpy(), pt
+
+
+# ---- binary16 encoders ---------------------------------------------------------
+
+def test_f16_encoders_bitexact(rkv, rko, ctx):
+    torch = _torch()
+    rng = np.random.default_rng(11)
+    bits = rng.integers(0, 2 ** 32, 60000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32).copy()
+    # scales d = amax/127 span small positive values: sample them densely
+    d = (rng.uniform(0, 1, 60000) * 2.0 ** rng.integers(-40, 18, 60000)).astype(np.float32)
+    edges = []
+    for k in range(-26, 17):
+        base = np.float32(2.0 ** k)
+        edges += [base, np.float32(base * (2 - 2.0 ** -11)), np.float32(base * (2 - 2.0 ** -12)),
+                  np.float32(base * (1 + 2.0 ** -11)), np.nextafter(base, np.float32(0))]
+    edges += [0.0, -0.0, np.inf, -np.inf, np.nan, 65504, 65520, 65519.99]
+    x = np.concatenate([x, d, -d[:1000], np.array(edges, np.float32)]).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    L = rko.lib()
+    for rule, fn in ((0, L.rko_f32_to_f16), (1, L.rko_f32_to_f16_harserve)):
+        out = torch.empty(x.size, dtype=torch.int16, device="cuda")
+        rkv.f32_to_f16(ctx, xd, out, rule)
+        ctx.sync()
+        got = out.cpu().numpy().view(np.uint16)
+        want = np.array([fn(float(v)) for v in x], np.uint16)
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, f"rule {rule}: {bad.size} mismatches, first x={x[bad[:3]]}"
+
+
+# ---- append / gather / import ----------------------------------------------------
+
+@pytest.mark.parametrize("D,PT,rule,bf16", [
+    (128, 16, 0, False), (256, 64, 0, True), (256, 64, 1, False), (256, 32, 0, False),
+    (128, 256, 1, True), (256, 16, 0, False)])
+def test_append_bitexact(rkv, rko, ctx, D, PT, rule, bf16):
+    print(f"append D={D} PT={PT} rule={rule} bf16={bf16}", flush=True)
+    sc = Scene(rkv, rko, 2, D, PT, [3 * PT + 7, 1, 2 * PT], seed=D + PT + rule, outliers=0.01,
+               src_bf16=bf16, rule=rule)
+    ctx.sync()
+    assert np.array_equal(sc.pages_d.cpu().numpy(), sc.pages), "page bytes differ"
+    torch = _torch()
+    for b, L in enumerate(sc.lens):
+        for kind, src in ((0, sc.k), (1, sc.v)):
+            out = torch.empty(2 * int(L) * rkv.row_bytes(D), dtype=torch.uint8, device="cuda")
+            rkv.gather_q8(ctx, sc.g, sc.pages_d, sc.bt_d[b], int(L), kind, out)
+            ctx.sync()
+            got = out.cpu().numpy().reshape(2, L, -1)
+            rows = src[sc.seq_ids == b]
+            for h in range(2):
+                want = rko.q8_quantize(rows[:, h, :].reshape(-1), rule).reshape(L, -1)
+                assert np.array_equal(got[h], want), f"seq {b} kind {kind} head {h}"
+
+
+def test_append_special_values(rkv, rko, ctx):
+    """Zero blocks, huge (f16-overflowing scale), tiny (subnormal scale), inf and
+    NaN inputs quantize identically on both sides, for both rules."""
+    torch = _torch()
+    D, PT, Hkv = 256, 64, 1
+    rng = np.random.default_rng(5)
+    rows = rng.standard_normal((6, Hkv, D)).astype(np.float32)
+    rows[0, 0, :32] = 0
+    rows[1, 0, :] *= np.float32(3e6)
+    rows[2, 0, :] *= np.float32(1e-9)
+    rows[3, 0, 5] = np.inf
+    rows[4, 0, 40] = np.nan
+    rows[5, 0, 64:96] = np.float32(2.0 ** -5 * (2 - 2.0 ** -12) * 127)  # carry window
+    for rule in (0, 1):
+        g = rkv.geometry(Hkv, D, PT, 2)
+        lay = rko.layout(Hkv, D, PT, 2)
+        bt = np.array([[1]], np.int32)
+        pages = np.zeros(2 * rkv.page_bytes(g), np.uint8)
+        sid = np.zeros(6, np.int32)
+        pos = np.arange(6, dtype=np.int32)
+        rko.paged_append(lay, pages, bt, sid, pos, rows, rows, rule)
+        pd = torch.zeros(pages.size, dtype=torch.uint8, device="cuda")
+        rkv.append_q8(ctx, g, pd, torch.from_numpy(bt).cuda(), torch.from_numpy(sid).cuda(),
+                      torch.from_numpy(pos).cuda(), torch.from_numpy(rows).cuda(),
+                      torch.from_numpy(rows).cuda(), rule=rule)
+        ctx.sync()
+        assert np.array_equal(pd.cpu().numpy(), pages), f"rule {rule}"
+
+
+@pytest.mark.parametrize("D,PT", [(128, 16), (256, 64), (256, 32)])
+def test_import_gather_roundtrip(rkv, rko, ctx, D, PT):
+    torch = _torch()
+    rng = np.random.default_rng(D * PT)
+    L, Hkv = 5 * PT + 3, 2
+    npg = (L + PT - 1) // PT
+    g = rkv.geometry(Hkv, D, PT, npg + 4)
+    bt = rng.permutation(npg + 4)[:npg].astype(np.int32)
+    rows = rng.integers(0, 256, (Hkv, L, rkv.row_bytes(D)), dtype=np.uint8)
+    pages = torch.zeros((npg + 4) * rkv.page_bytes(g), dtype=torch.uint8, device="cuda")
+    btd = torch.from_numpy(bt).cuda()
+    rd = torch.from_numpy(rows).cuda()
+    for kind in (0, 1):
+        rkv.import_q8(ctx, g, pages, btd, L, kind, rd)
+        out = torch.empty_like(rd)
+        rkv.gather_q8(ctx, g, pages, btd, L, kind, out)
+        ctx.sync()
+        assert np.array_equal(out.cpu().numpy(), rows)
+    # the oracle reads the same page bytes back the same way
+    lay = rko.layout(Hkv, D, PT, npg + 4)
+    got = rko.paged_gather(lay, pages.cpu().numpy(), bt, L, 1)
+    assert np.array_equal(got, rows)
+
+
+# ---- decode ------------------------------------------------------------------------
+
+def test_config1_decode(rkv, rko, ctx):
+    """1 sequence, Hq 8 / Hkv 2, D 128, 16-token pages, 2048
+    context, f32 K/V and q ~ N(0,1), scale 1/sqrt(128), seeded permutation."""
+    sc = Scene(rkv, rko, 2, 128, 16, [2048], seed=0)
+    rng = np.random.default_rng(100)
+    q = rng.standard_normal((1, 1, 8, 128)).astype(np.float32)
+    scale = 1.0 / math.sqrt(128)
+    for pt_req in (0, 256, 1024):
+        got, pt = _run_decode(rkv, ctx, sc, q, scale, partition_tokens=pt_req)
+        want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(1, dtype=np.int32),
+                                q, scale, pt)
+        assert_close(got, want, what=f"config1 pt={pt}")
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,PT,lens,q_bf16,out_bf16", [
+    (16, 2, 256, 64, [4100, 700, 33, 1, 2000], True, False),
+    (16, 2, 256, 32, [1500, 31, 64], True, False),
+    (8, 4, 256, 64, [1024, 999], False, False),
+    (4, 4, 128, 16, [517, 64, 1], False, True),
+    (32, 2, 128, 128, [3000], True, False),
+])
+def test_decode_parity(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_bf16, out_bf16):
+    print(f"decode Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens}", flush=True)
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=Hq + D + PT, outliers=0.01, src_bf16=True)
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((len(lens), 1, Hq, D)).astype(np.float32)
+    if q_bf16:
+        q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    scale = 1.0 / math.sqrt(D)
+    got, pt = _run_decode(rkv, ctx, sc, q, scale, q_bf16=q_bf16, out_bf16=out_bf16)
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(len(lens), dtype=np.int32),
+                            q, scale, pt)
+    if out_bf16:
+        # the f32 result rounded once to bf16 (half an ulp = 2^-9 relative)
+        err = np.abs(got - want) - np.abs(want) * 2.0 ** -8
+        assert float(err.max()) <= ATOL
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) <= RTOL + 2.0 ** -8
+    else:
+        assert_close(got, want, what=f"decode pt={pt}")
+
+
+def test_smoke_mirror(rkv, rko, ctx):
+    """har-serve-vulkan-attn-smoke.rs:41-185 with its inputs (lcg K/V, har-serve
+    quantizer, seq_len 1024, 8 q heads / 4 kv heads, no scale), through the
+    flash_decode_q8.comp drop-in entry point; the smoke passes at max-abs <= 1e-3."""
+    torch = _torch()
+    S, Hq, Hkv, D = 1024, 8, 4, 256
+    rb = rko.row_bytes(D)
+    k = np.empty((Hkv, S, rb), np.uint8)
+    v = np.empty_like(k)
+    for h in range(Hkv):
+        for p in range(S):
+            k[h, p] = rko.q8_quantize_harserve(rko.lcg_values(D, 1000 + (h * S + p) * 31))
+            v[h, p] = rko.q8_quantize_harserve(rko.lcg_values(D, 2000 + (h * S + p) * 17))
+    kw, vw = rko.rows_to_words(k), rko.rows_to_words(v)
+    query = rko.lcg_values(Hq * D, 3000)
+    p = rko.fd_params(Hq, Hkv, S, 1024, D)
+    want = rko.flash_decode_reference(p, kw, vw, query)
+    rp = rkv.FlashDecodeParams(Hq, Hkv, S, 1024, D)
+    scratch = torch.empty(rkv.flash_decode_scratch_bytes(rp), dtype=torch.uint8, device="cuda")
+    out = torch.empty(Hq * D, dtype=torch.float32, device="cuda")
+    rkv.flash_decode_q8(ctx, rp, torch.from_numpy(kw.view(np.int32)).cuda(),
+                        torch.from_numpy(vw.view(np.int32)).cuda(), torch.from_numpy(query).cuda(),
+                        out, scratch)
+    ctx.sync()
+    got = out.cpu().numpy()
+    assert float(np.max(np.abs(got - want))) <= 1e-3
+    assert_close(got, want, what="smoke")
+
+
+def test_splitk_partials_and_combine(rkv, rko, ctx):
+    """Per-partition (m, l, o) equal the oracle's per-chunk partials
+    (attention.rs:182-204); the combine reproduces attention.rs:205-212."""
+    torch = _torch()
+    Hq, Hkv, D, PT = 8, 2, 256, 64
+    sc = Scene(rkv, rko, Hkv, D, PT, [1000, 260], seed=3)
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((2, 1, Hq, D)).astype(np.float32)
+    scale = 1.0 / 16
+    part = 256
+    n_parts = 4
+    qd = torch.from_numpy(q).cuda()
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    sid = torch.arange(2, dtype=torch.int32, device="cuda")
+    a = rkv.decode_args(qd, out, sid, scale, 1000, partition_tokens=part)
+    ml = torch.full((2, Hq, n_parts, 2), float("nan"), device="cuda")
+    o = torch.full((2, Hq, n_parts, D), float("nan"), device="cuda")
+    rkv.decode_q8_partials(ctx, sc.g, sc.pages_d, sc.bt_d, sc.lens_d, a, ml, o)
+    ctx.sync()
+    mln, on = ml.cpu().numpy(), o.cpu().numpy()
+    log2e = 1.0 / math.log(2.0)
+    for b, L in enumerate(sc.lens):
+        kr = rko.paged_gather(sc.lay, sc.pages, sc.bt[b], int(L), 0)
+        vr = rko.paged_gather(sc.lay, sc.pages, sc.bt[b], int(L), 1)
+        kw, vw = rko.rows_to_words(kr), rko.rows_to_words(vr)
+        for h in range(Hq):
+            kvh = h // (Hq // Hkv)
+            off = kvh * int(L) * rko.row_bytes(D) // 4
+            p = rko.fd_params(Hq, Hkv, int(L), part, D)
+            qs = (q[b, 0, h] * np.float32(scale)).astype(np.float32)
+            cm, lc, oc = rko.flash_decode_partials(p, kw[off:], vw[off:], qs, 0)
+            np_b = len(cm)
+            assert np_b == (int(L) + part - 1) // part
+            assert np.allclose(mln[b, h, :np_b, 0], cm * log2e, atol=2e-3, rtol=1e-4)
+            assert np.allclose(mln[b, h, :np_b, 1], lc, rtol=2e-3, atol=1e-3)
+            # o relative to the partition's weight mass
+            for i in range(np_b):
+                assert_close(on[b, h, i] / lc[i], oc[i] / lc[i], what=f"partial b{b} h{h} p{i}")
+    comb = torch.empty_like(out)
+    rkv.splitk_combine(ctx, ml, o, 2, Hq, n_parts, D, sid, sc.lens_d, part, comb)
+    direct, _ = _run_decode(rkv, ctx, sc, q, scale, partition_tokens=part)
+    ctx.sync()
+    assert np.array_equal(comb.cpu().numpy(), direct)
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(2, dtype=np.int32), q,
+                            scale, part)
+    assert_close(direct, want, what="combine")
+
+
+def test_verify_causal(rkv, rko, ctx):
+    """q_len=4 causal verify: draft row j attends positions [0, ctx+j]; equal to
+    the oracle and to single-row decodes of length ctx+j+1 (attention.rs:169-215)."""
+    torch = _torch()
+    Hq, Hkv, D, PT, ctx_len, ql = 16, 2, 256, 64, 1500, 4
+    lens = [ctx_len + ql, 70 + ql, 33]
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=21, src_bf16=True)
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((3, ql, Hq, D)).astype(np.float32)
+    q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    scale = 1.0 / 16
+    got, pt = _run_decode(rkv, ctx, sc, q, scale, q_bf16=True, q_len=ql)
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(3, dtype=np.int32), q,
+                            scale, pt)
+    assert_close(got, want, what=f"verify pt={pt}")
+    # row j == a decode over the first len-ql+j+1 positions
+    for j in range(ql):
+        lens_j = torch.from_numpy(sc.lens - ql + j + 1).cuda()
+        qj = torch.from_numpy(np.ascontiguousarray(q[:, j:j + 1])).cuda().to(torch.bfloat16)
+        out = torch.empty(qj.shape, dtype=torch.float32, device="cuda")
+        sid = torch.arange(3, dtype=torch.int32, device="cuda")
+        a = rkv.decode_args(qj, out, sid, scale, int(sc.lens.max()), partition_tokens=pt)
+        ws = torch.empty(max(rkv.decode_workspace_bytes(sc.g, a), 4), dtype=torch.uint8, device="cuda")
+        a = rkv.decode_args(qj, out, sid, scale, int(sc.lens.max()), partition_tokens=pt, workspace=ws)
+        rkv.decode_q8(ctx, sc.g, sc.pages_d, sc.bt_d, lens_j, a)
+        ctx.sync()
+        assert_close(got[:, j:j + 1], out.cpu().numpy(), atol=1e-5, rtol=1e-5, what=f"row {j}")
+
+
+def test_decode_edge_lengths(rkv, rko, ctx):
+    """len 0 -> zeros (flash_decode_q8.comp:144-148); len 1 -> dequant(V_0);
+    lengths around tile and partition boundaries."""
+    Hq, Hkv, D, PT = 8, 2, 128, 32
+    lens = [0, 1, 31, 32, 33, 255, 256, 257]
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=2)
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal((len(lens), 1, Hq, D)).astype(np.float32)
+    got, pt = _run_decode(rkv, ctx, sc, q, 0.1, partition_tokens=64)
+    assert pt == 64
+    assert np.all(got[0] == 0.0)
+    v0 = rko.paged_gather(sc.lay, sc.pages, sc.bt[1], 1, 1)
+    for h in range(Hq):
+        want = rko.q8_decode(v0[h // 4, 0], D)
+        assert_close(got[1, 0, h], want, atol=1e-3, rtol=1e-3, what="len1")
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(len(lens), dtype=np.int32),
+                            q, 0.1, pt)
+    want[0] = 0.0
+    assert_close(got, want, what="edges")
+
+
+def test_bad_block_table_is_reported(rkv, rko, ctx):
+    """An out-of-pool page id never leaves the pool on the device and makes the
+    next rkv_ctx_sync fail with RKV_ERR_BAD_BLOCK_TABLE."""
+    torch = _torch()
+    sc = Scene(rkv, rko, 2, 128, 16, [100], seed=1)
+    ctx.sync()
+    bad = sc.bt.copy()
+    bad[0, 3] = sc.num_pages + 5
+    sc.bt_d = torch.from_numpy(bad).cuda()
+    q = np.ones((1, 1, 4, 128), np.float32)
+    with pytest.raises(rkv.RkvError) as e:
+        _run_decode(rkv, ctx, sc, q, 1.0)
+    assert e.value.status == rkv.ERR_BAD_BLOCK_TABLE
+    ctx.sync()  # the fault word was cleared
+    k = torch.zeros((1, 2, 128), device="cuda")
+    bad[0, 0] = -1
+    with pytest.raises(rkv.RkvError) as e:
+        rkv.append_q8(ctx, sc.g, sc.pages_d, torch.from_numpy(bad).cuda(),
+                      torch.zeros(1, dtype=torch.int32, device="cuda"),
+                      torch.zeros(1, dtype=torch.int32, device="cuda"), k, k)
+        ctx.sync()
+    assert e.value.status == rkv.ERR_BAD_BLOCK_TABLE
+
+
+def test_pool_api_and_rollback(rkv, rko, ctx):
+    """Operator-level API: allocator-driven pool, append, decode, gather; a
+    speculative rollback (truncate) followed by re-append gives the same bytes
+    as appending the accepted rows directly."""
+    torch = _torch()
+    Hkv, D, PT, Hq = 2, 256, 64, 16
+    pool = rkv.Pool(ctx, 2, Hkv, D, PT, 64, 4, 16, seed=5)
+    rng = np.random.default_rng(12)
+    L0 = 200
+    pool.alloc.reserve(0, L0)
+    pool.alloc.reserve(1, 90)
+    pool.sync_tables()
+    rows0 = rng.standard_normal((L0, Hkv, D)).astype(np.float32)
+    rows1 = rng.standard_normal((90, Hkv, D)).astype(np.float32)
+    for layer in (0, 1):
+        for s, rows in ((0, rows0), (1, rows1)):
+            n = rows.shape[0]
+            pool.append(layer, torch.full((n,), s, dtype=torch.int32, device="cuda"),
+                        torch.arange(n, dtype=torch.int32, device="cuda"),
+                        torch.from_numpy(rows * (layer + 1)).cuda(),
+                        torch.from_numpy(rows * (layer + 1)).cuda())
+    # speculative: append 4 draft rows to seq 0, accept 1, roll back the rest
+    draft = rng.standard_normal((4, Hkv, D)).astype(np.float32)
+    pool.alloc.reserve(0, L0 + 4)
+    pool.sync_tables()
+    pool.append(0, torch.zeros(4, dtype=torch.int32, device="cuda"),
+                torch.arange(L0, L0 + 4, dtype=torch.int32, device="cuda"),
+                torch.from_numpy(draft).cuda(), torch.from_numpy(draft).cuda())
+    pool.alloc.truncate(0, L0 + 1)
+    nxt = rng.standard_normal((1, Hkv, D)).astype(np.float32)
+    pool.alloc.reserve(0, L0 + 2)
+    pool.sync_tables()
+    pool.append(0, torch.zeros(1, dtype=torch.int32, device="cuda"),
+                torch.full((1,), L0 + 1, dtype=torch.int32, device="cuda"),
+                torch.from_numpy(nxt).cuda(), torch.from_numpy(nxt).cuda())
+    ctx.sync()
+    accepted = np.concatenate([rows0, draft[:1], nxt])
+    out = torch.empty(Hkv * (L0 + 2) * rkv.row_bytes(D), dtype=torch.uint8, device="cuda")
+    pool.gather(0, 0, 0, out)
+    ctx.sync()
+    got = out.cpu().numpy().reshape(Hkv, L0 + 2, -1)
+    for h in range(Hkv):
+        assert np.array_equal(got[h], rko.q8_encode(accepted[:, h, :].reshape(-1)).reshape(L0 + 2, -1))
+    # decode through the pool equals the oracle over the gathered rows
+    q = rng.standard_normal((2, 1, Hq, D)).astype(np.float32)
+    qd = torch.from_numpy(q).cuda()
+    o = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    sid = torch.tensor([0, 1], dtype=torch.int32, device="cuda")
+    a = rkv.decode_args(qd, o, sid, 1 / 16, 16 * PT, partition_tokens=256)
+    ws = torch.empty(max(rkv.decode_workspace_bytes(pool.geometry, a), 4), dtype=torch.uint8,
+                     device="cuda")
+    a = rkv.decode_args(qd, o, sid, 1 / 16, 16 * PT, partition_tokens=256, workspace=ws)
+    pool.decode(0, a)
+    ctx.sync()
+    tables, lens = pool.alloc.export()
+    pages0 = _as_u8(pool.layer_pages(0), 64 * rkv.page_bytes(pool.geometry)).clone()
+    lay = rko.layout(Hkv, D, PT, 64)
+    want = rko.paged_decode(lay, pages0.cpu().numpy(), tables, lens, np.array([0, 1], np.int32), q,
+                            1 / 16, 256)
+    assert_close(o.cpu().numpy(), want, what="pool decode")
+    pool.close()
+
+
+def _as_u8(ptr, n):
+    """A uint8 torch view of n bytes of device memory owned by the pool."""
+    torch = _torch()
+
+    class _Holder:
+        __cuda_array_interface__ = {"shape": (n,), "typestr": "|u1", "data": (ptr, False),
+                                    "version": 3}
+    return torch.as_tensor(_Holder(), device="cuda")
