@@ -283,11 +283,13 @@ def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0
     import torch
     B = seq_ids.numel()
     q_heads = q.shape[-2]
-    return DecodeArgs(B, _ptr(seq_ids), _ptr(q), BF16 if q.dtype == torch.bfloat16 else F32,
-                      q_len, q_heads, scale, _ptr(out),
-                      BF16 if out.dtype == torch.bfloat16 else F32, partition_tokens,
-                      max_seq_len, _ptr(workspace),
-                      0 if workspace is None else workspace.numel() * workspace.element_size())
+    a = DecodeArgs(B, _ptr(seq_ids), _ptr(q), BF16 if q.dtype == torch.bfloat16 else F32,
+                   q_len, q_heads, scale, _ptr(out),
+                   BF16 if out.dtype == torch.bfloat16 else F32, partition_tokens,
+                   max_seq_len, _ptr(workspace),
+                   0 if workspace is None else workspace.numel() * workspace.element_size())
+    a._refs = (q, out, seq_ids, workspace)  # the struct holds raw device pointers
+    return a
 
 
 def decode_workspace_bytes(g: Geometry, a: DecodeArgs) -> int:
