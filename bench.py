@@ -18,6 +18,7 @@ path (the C restatement in oracle/) timed on a bounded sample on this host.
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import importlib.util
 import json
 import math
@@ -129,29 +130,41 @@ def main() -> int:
     part = rkv.decode_partition_tokens(g, a)
     n_parts = (L + part - 1) // part
     rows = Hq
+    # split-K partials, laid out as rkv_decode_q8's workspace
     ml = torch.empty((B, rows, n_parts, 2), device=dev, dtype=torch.float32)
-    o_ws = torch.empty((B, rows, n_parts, D), device=dev, dtype=torch.float32)
-    lens_ptr = pool.seq_lens_ptr()
-    bt_ptr = pool.block_tables_ptr()
-    pages_ptr = pool.layer_pages(0)
+    o = torch.empty((B, rows, n_parts, D), device=dev, dtype=torch.float32)
     stream = torch.cuda.current_stream()
-    L_ = rkv.lib()
-    C = rkv.C
+    lib = rkv.lib()
+    pages_p = pool.layer_pages(0)
+    bt_p = pool.block_tables_ptr()
+    lens_p = pool.seq_lens_ptr()
 
     def step(ev=None):
+        # rkv_pool_append, then the two kernels rkv_pool_decode chains
+        # (split-K decode, log-sum-exp combine), called through their
+        # kernel-level entry points so events can bracket each kernel
         if ev is not None:
             ev[0].record(stream)
         pool.append(0, seq_ids, positions, k_new, v_new, stream=stream)
         if ev is not None:
             ev[1].record(stream)
-        rkv.check(L_.rkv_decode_q8_partials(ctx.h, C.byref(g), rkv.P(pages_ptr), rkv.P(bt_ptr),
-                                            pages_per_seq, rkv.P(lens_ptr), B, C.byref(a),
-                                            rkv._ptr(ml), rkv._ptr(o_ws), rkv._stream(stream)))
-        if ev is not None:
-            ev[2].record(stream)
-        rkv.check(L_.rkv_splitk_combine(ctx.h, rkv._ptr(ml), rkv._ptr(o_ws), B, rows, n_parts, D,
-                                        rkv._ptr(seq_ids), rkv.P(lens_ptr), B, part,
-                                        rkv._ptr(out), rkv.F32, rkv._stream(stream)))
+        if n_parts > 1:
+            rkv.check(lib.rkv_decode_q8_partials(ctx.h, C.byref(g), C.c_void_p(pages_p),
+                                                 C.c_void_p(bt_p), pages_per_seq,
+                                                 C.c_void_p(lens_p), B, C.byref(a),
+                                                 C.c_void_p(ml.data_ptr()), C.c_void_p(o.data_ptr()),
+                                                 C.c_void_p(stream.cuda_stream)))
+            if ev is not None:
+                ev[2].record(stream)
+            rkv.check(lib.rkv_splitk_combine(ctx.h, C.c_void_p(ml.data_ptr()),
+                                             C.c_void_p(o.data_ptr()), B, rows, n_parts, D,
+                                             C.c_void_p(seq_ids.data_ptr()), C.c_void_p(lens_p), B,
+                                             part, C.c_void_p(out.data_ptr()), rkv.F32,
+                                             C.c_void_p(stream.cuda_stream)))
+        else:
+            pool.decode(0, a, stream=stream)
+            if ev is not None:
+                ev[2].record(stream)
         if ev is not None:
             ev[3].record(stream)
 
@@ -181,8 +194,10 @@ def main() -> int:
     bt_bytes = B * pages_per_seq * 4
     app_bytes = B * Hkv * 2 * (D * 2 + row)
     step_bytes = kv_bytes + q_bytes + out_bytes + bt_bytes + app_bytes
-    dec_bytes = kv_bytes + q_bytes + bt_bytes
     partial_bytes = B * rows * n_parts * (D + 2) * 4
+    # the decode kernel reads K/V, q and the block tables and writes the
+    # partials (or `out` when one partition covers the sequence)
+    dec_bytes = kv_bytes + q_bytes + bt_bytes + (partial_bytes if n_parts > 1 else out_bytes)
     flops = 4 * D * Hq * B * L
 
     value = step_bytes / step_s / 1e9

@@ -143,8 +143,9 @@ typedef struct rkv_decode_args {
   int32_t partition_tokens; /* split-K partition length: a multiple of max(32,
                                page_tokens), at most 64*page_tokens; 0 = auto */
   int32_t max_seq_len;      /* >= every seq_lens[seq_ids[b]]; sizes the grid */
-  void *workspace;          /* device scratch for split-K partials (may be NULL
-                               when one partition covers every sequence) */
+  void *workspace;          /* device scratch for the split-K partials, of
+                               rkv_decode_workspace_bytes (may be NULL when one
+                               partition covers every sequence) */
   size_t workspace_bytes;
 } rkv_decode_args;
 
@@ -163,7 +164,7 @@ rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
  * flash_decode_reference / flash_decode_online (attention.rs:148-215) and
  * the flash_decode_q8.comp dispatch (har-serve-vulkan-attn-smoke.rs:149-161).
  * With more than one partition per sequence the partials go to `workspace`
- * and the combine runs on the same stream. */
+ * and a second kernel merges them (rkv_splitk_combine's algebra). */
 rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                          const int32_t *block_tables, int32_t bt_stride,
                          const int32_t *seq_lens, int32_t n_seqs,

@@ -22,10 +22,18 @@ def build() -> str:
     return _SO
 
 
+def _stale() -> bool:
+    if not os.path.exists(_SO):
+        return True
+    so = os.path.getmtime(_SO)
+    return any(os.path.getmtime(os.path.join(_HERE, f)) > so
+               for f in ("rkv_oracle.c", "rkv_oracle.h", "Makefile"))
+
+
 def lib():
     global _lib
     if _lib is None:
-        if not os.path.exists(_SO):
+        if _stale():
             build()
         _lib = C.CDLL(_SO)
         _declare(_lib)

@@ -538,8 +538,9 @@ void rko_attention_f64(int32_t seq_len, int32_t head_dim, const uint32_t *k_word
  * region = codes (page_tokens*D bytes) then scales (page_tokens*D/32 f16).
  *   K codes: [slot][dim]                         (row-major, as the reference row)
  *   V codes: [slot/TT][dim][slot%TT]             (dim-major inside TT-slot tiles)
- *   scales : [slot/TT][block][slot%TT]  (K and V)
- * with TT = min(32, page_tokens).  Restated here independently of the HIP
+ *   scales : [slot/TT][block][pos(slot%TT)]  (K and V)
+ * with TT = min(32, page_tokens); for TT == 32, pos(16m + 4g + r) = 8g + 4m + r
+ * (m<2, g<4, r<4), for TT == 16 pos(t) = t.  Restated here independently of the HIP
  * source so the checker does not share code with the product. */
 
 static int32_t tile_tokens(const rko_layout *L) {
@@ -561,9 +562,13 @@ size_t rko_code_offset(const rko_layout *L, int kind, int32_t slot, int32_t dim)
 size_t rko_scale_offset(const rko_layout *L, int32_t slot, int32_t block) {
   const int32_t TT = tile_tokens(L);
   const size_t nb = (size_t)(L->head_dim / 32);
+  int32_t t = slot % TT;
+  if (TT == 32) {
+    int32_t m = t / 16, g = (t / 4) % 4, r = t % 4;
+    t = 8 * g + 4 * m + r;
+  }
   return (size_t)L->page_tokens * (size_t)L->head_dim +
-         2 * ((size_t)(slot / TT) * nb * (size_t)TT + (size_t)block * (size_t)TT +
-              (size_t)(slot % TT));
+         2 * ((size_t)(slot / TT) * nb * (size_t)TT + (size_t)block * (size_t)TT + (size_t)t);
 }
 static size_t region_base(const rko_layout *L, int32_t page, int32_t kvh, int kind) {
   return (size_t)page * rko_page_bytes(L) + (size_t)(kvh * 2 + kind) * rko_region_bytes(L);

@@ -43,7 +43,6 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 constexpr int kTile = 32;    // tokens per tile
-constexpr int kStages = 2;   // LDS ring depth
 // s_waitcnt immediate with expcnt/lgkmcnt at their maxima (no wait) and
 // vmcnt = 0; OR in vmcnt bits [3:0] and [5:4] (at 15:14) to wait for less.
 constexpr int kWaitBase = 0x0f70;
@@ -87,60 +86,96 @@ __device__ __forceinline__ v4f f16x4_to_f32(uint2 w) {
   return r;
 }
 
-// Global source offsets of the 16-byte LDS chunks one lane copies per tile.
-// `half` says which 16-token half of the tile a chunk belongs to (the page
-// of that half is looked up per tile); `mul` scales the tile's starting
-// slot into the region (D for code runs, D/16 for scale runs).
+// Per-lane copy plan of one tile: source offsets (relative to the kv head's
+// base in the page of the chunk's 16-token half) of the LDS chunks this lane
+// copies.  Pages of >= 32 tokens hold the whole tile in one page laid out
+// exactly like the LDS stage, so the copy is S::kInstr 16-byte instructions
+// over the stage in order (the last one padded by re-reading chunk 0).
+// 16-token pages hold half a tile each: the code runs are still 16-byte
+// copies, but the lane-ordered scale runs interleave the two pages every 4
+// bytes, so they use 4-byte copies.
 template <int D, bool kSmallPage>
 struct ChunkPlan {
   using S = StageShape<D>;
-  uint32_t off[S::kInstr];
-  uint32_t mul[S::kInstr];  // D for code runs, D/16 for scale runs
-  uint32_t halves;          // bit k: chunk k lies in the tile's second 16-token half
+  static constexpr int kNKC = D / 32;                       // 1 KiB K-code (or V-code) copies
+  static constexpr int kN16 = kSmallPage ? 2 * kNKC : S::kInstr;
+  static constexpr int kN4 = kSmallPage ? 2 * (D / 128) : 0;  // 256-byte scale copies
+  static constexpr int kInstr = kN16 + kN4;                  // vmcnt units per tile
+  uint32_t off[kN16 + kN4];
+  uint32_t mul[kN16 + kN4];  // D for code runs, D/16 for scale runs (pages >= 32 tokens)
+  uint32_t halves;           // bit k: chunk k lies in the tile's second 16-token half
+  __host__ __device__ static constexpr int dst16(int k) {  // LDS byte offset of 16-B copy k
+    return kSmallPage ? (k < kNKC ? S::kKC + 1024 * k : S::kVC + 1024 * (k - kNKC)) : 1024 * k;
+  }
+  __host__ __device__ static constexpr int dst4(int k) {  // LDS byte offset of 4-B copy k
+    return k < kN4 / 2 ? S::kKS + 256 * k : S::kVS + 256 * (k - kN4 / 2);
+  }
 };
 
 template <int D, bool kSmallPage>
 __device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage> &pl, const Geo &g, int lane) {
   using S = StageShape<D>;
+  using PL = ChunkPlan<D, kSmallPage>;
   const uint32_t RB = (uint32_t)region_bytes(g);
   const uint32_t PTD = (uint32_t)g.page_tokens * D;
-  const uint32_t TT = (uint32_t)tile_tokens(g.page_tokens);
   pl.halves = 0;
+  if constexpr (!kSmallPage) {
 #pragma unroll
-  for (int k = 0; k < S::kInstr; ++k) {
-    const int c = 64 * k + lane;
-    uint32_t off = 0;
-    uint32_t half = 0, is_scale = 0;
-    if (c < 2 * D) {  // K codes: row r, physical chunk pc holds logical chunk pc ^ (r mod CPR)
-      const int r = c / S::kCPR;
-      const int pc = c % S::kCPR;
-      const int lc = pc ^ (r & (S::kCPR - 1));
-      half = r >= 16;
-      off = (uint32_t)((kSmallPage ? (r & 15) : r) * D + 16 * lc);
-    } else if (c < 2 * D + D / 8) {  // K scales: block b, tokens 8*piece..+7
-      const int i = c - 2 * D;
-      const int b = i >> 2, piece = i & 3;
-      half = piece >= 2;
-      is_scale = 1;
-      off = PTD + 2u * ((uint32_t)b * TT + (uint32_t)(kSmallPage ? 8 * (piece & 1) : 8 * piece));
-    } else if (c < 4 * D + D / 8) {  // V codes: dim row d, 16-token piece (halves swapped when (d>>2)&1)
-      const int i = c - (2 * D + D / 8);
-      const int d = i >> 1;
-      const int lh = (i & 1) ^ ((d >> 2) & 1);
-      half = lh;
-      off = RB + (uint32_t)d * TT + (uint32_t)(kSmallPage ? 0 : 16 * lh);
-    } else if (c < 4 * D + D / 4) {  // V scales
-      const int i = c - (4 * D + D / 8);
-      const int b = i >> 2, piece = i & 3;
-      half = piece >= 2;
-      is_scale = 1;
-      off = RB + PTD + 2u * ((uint32_t)b * TT + (uint32_t)(kSmallPage ? 8 * (piece & 1) : 8 * piece));
-    } else {  // padding lanes of the last instruction: re-read chunk 0 of the tile
-      off = 0;
+    for (int k = 0; k < S::kInstr; ++k) {
+      const int c = 64 * k + lane;
+      uint32_t off = 0, is_scale = 0;
+      if (c < 2 * D) {  // K codes: row r, physical chunk pc holds logical chunk pc ^ (r mod CPR)
+        const int r = c / S::kCPR;
+        const int lc = (c % S::kCPR) ^ (r & (S::kCPR - 1));
+        off = (uint32_t)(r * D + 16 * lc);
+      } else if (c < 2 * D + D / 8) {  // K scales: block b, lane-ordered positions 8*j..8*j+7
+        const int i = c - 2 * D;
+        off = PTD + 2u * (uint32_t)(32 * (i >> 2) + 8 * (i & 3));
+        is_scale = 1;
+      } else if (c < 4 * D + D / 8) {  // V codes: dim row d, 16-token piece (halves swapped when (d>>2)&1)
+        const int i = c - (2 * D + D / 8);
+        const int d = i >> 1;
+        const int lh = (i & 1) ^ ((d >> 2) & 1);
+        off = RB + (uint32_t)(d * 32 + 16 * lh);
+      } else if (c < 4 * D + D / 4) {  // V scales
+        const int i = c - (4 * D + D / 8);
+        off = RB + PTD + 2u * (uint32_t)(32 * (i >> 2) + 8 * (i & 3));
+        is_scale = 1;
+      }  // else: padding lane of the last copy, re-reads chunk 0 of the tile
+      pl.off[k] = off;
+      pl.mul[k] = is_scale ? (uint32_t)(D / 16) : (uint32_t)D;
     }
-    pl.off[k] = off;
-    pl.mul[k] = is_scale ? (uint32_t)(D / 16) : (uint32_t)D;
-    pl.halves |= half << k;
+  } else {
+#pragma unroll
+    for (int k = 0; k < PL::kN16; ++k) {
+      const int c = 64 * (k % PL::kNKC) + lane;
+      uint32_t off, half;
+      if (k < PL::kNKC) {  // K codes
+        const int r = c / S::kCPR;
+        const int lc = (c % S::kCPR) ^ (r & (S::kCPR - 1));
+        half = r >= 16;
+        off = (uint32_t)((r & 15) * D + 16 * lc);
+      } else {  // V codes [d][16] per page
+        const int d = c >> 1;
+        half = (c & 1) ^ ((d >> 2) & 1);
+        off = RB + (uint32_t)d * 16u;
+      }
+      pl.off[k] = off;
+      pl.mul[k] = 0;
+      pl.halves |= half << k;
+    }
+#pragma unroll
+    for (int k = 0; k < PL::kN4; ++k) {
+      // dword w of a kind's scale run: block b, lane-ordered positions p, p+1
+      const int kind = k < PL::kN4 / 2 ? 0 : 1;
+      const int w = 64 * (k % (PL::kN4 / 2)) + lane;
+      const int b = w >> 4, p = 2 * (w & 15);
+      const uint32_t half = (p >> 2) & 1;
+      const uint32_t tk = (uint32_t)(4 * (p >> 3) + (p & 3));
+      pl.off[PL::kN16 + k] = (kind ? RB : 0u) + PTD + 2u * ((uint32_t)b * 16u + tk);
+      pl.mul[PL::kN16 + k] = 0;
+      pl.halves |= half << (PL::kN16 + k);
+    }
   }
 }
 
@@ -153,8 +188,13 @@ __device__ __forceinline__ T lds_load(const lds_u8 *p) {
   return *reinterpret_cast<const __attribute__((address_space(3))) T *>(p);
 }
 
+// Rescale threshold (base-2 log units): the running reference max of a row
+// only moves when a tile's max exceeds it by more than kTau, so p = 2^(s-m)
+// stays <= 2^kTau and the accumulators are rescaled only a few times.
+constexpr float kTau = 4.0f;
+
 // One workgroup's decode of one (partition, batch entry, kv head).
-template <int D, int NT, bool kSmall>
+template <int D, int NT, bool kSmall, int NS>
 struct Decoder {
   using S = StageShape<D>;
   static constexpr int NP = (NT + 1) / 2;  // PV n-tiles of 16 rows
@@ -173,24 +213,25 @@ struct Decoder {
   float rmul[NP];
   int32_t rlim[NP];
   v4f oacc[NP][D / 16];
-  float mrun[NP], lrun[NP];
+  float mref[NP], lrun[NP];
 
   __device__ __forceinline__ Decoder(const DecodeLaunch &p_) : p(p_) {}
 
   // Copy tile `tile` (32 tokens) of this work unit HBM -> LDS stage `dst`.
   // Page ids come from `pidv` (lane i holds the partition's i-th page id).
-  __device__ __forceinline__ void issue(int tile, lds_u8 *__restrict__ dst) {
+  __device__ __forceinline__ void issue(int tile, lds_u8 *dst) {
     const Geo &g = p.g;
     const int32_t t0 = tok0 + tile * kTile;
     const int32_t pi = t0 / g.page_tokens - pg_first;
+    using PL = ChunkPlan<D, kSmall>;
     if constexpr (!kSmall) {
       const int32_t pid = __builtin_amdgcn_readlane(pidv, pi);
       const uint8_t *base = kv_base + (uint64_t)pid * PB;
       const uint32_t s0 = (uint32_t)(t0 % g.page_tokens);
 #pragma unroll
-      for (int k = 0; k < S::kInstr; ++k) {
+      for (int k = 0; k < PL::kN16; ++k) {
         const uint32_t voff = plan.off[k] + s0 * plan.mul[k];
-        __builtin_amdgcn_global_load_lds(base + voff, dst + 1024 * k, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(base + voff, dst + PL::dst16(k), 16, 0, 0);
       }
     } else {
       // 16-token pages: the two halves of the tile live in two pages
@@ -199,17 +240,22 @@ struct Decoder {
       const uint8_t *base0 = kv_base + (uint64_t)pid0 * PB;
       const uint8_t *base1 = kv_base + (uint64_t)pid1 * PB;
 #pragma unroll
-      for (int k = 0; k < S::kInstr; ++k) {
+      for (int k = 0; k < PL::kN16; ++k) {
         const bool h = (plan.halves >> k) & 1u;
-        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[k], dst + 1024 * k, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[k], dst + PL::dst16(k), 16, 0, 0);
+      }
+#pragma unroll
+      for (int k = 0; k < PL::kN4; ++k) {
+        const bool h = (plan.halves >> (PL::kN16 + k)) & 1u;
+        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[PL::kN16 + k], dst + PL::dst4(k), 4, 0, 0);
       }
     }
   }
 
   // Scores, online softmax and PV for the tile held in LDS stage `st`.
-  __device__ __forceinline__ void compute(int tile, const lds_u8 *__restrict__ st) {
+  __device__ __forceinline__ void compute(int tile, const lds_u8 *st) {
     const int32_t t0 = tok0 + tile * kTile;
-    // ---- QK^T ----
+    // ---- QK^T: int32 block dots, scaled by the f16 K scale of (token, block) ----
     float sacc[NT][2][4];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
@@ -225,20 +271,24 @@ struct Decoder {
         const int pc = (4 * c + lg) ^ (krow & (S::kCPR - 1));
         const v4i a = lds_load<v4i>(st + S::kKC + krow * D + 16 * pc);
         const int blk = 2 * c + (li >> 3);
-        const v4f dk = f16x4_to_f32(lds_load<uint2>(st + S::kKS + 2 * (blk * 32 + 16 * mt + 4 * lg)));
+        // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
+        const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
+        const float dk[4] = {(float)dk8[4 * mt], (float)dk8[4 * mt + 1], (float)dk8[4 * mt + 2],
+                             (float)dk8[4 * mt + 3]};
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const v4i z = {0, 0, 0, 0};
           const v4i ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[nt][c], z, 0, 0, 0);
           const v4i cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[nt][c], z, 0, 0, 0);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) sacc[nt][mt][r] += (float)((ch[r] << 7) + cl[r]) * dk[r];
+          for (int r = 0; r < 4; ++r)
+            sacc[nt][mt][r] = __builtin_fmaf((float)((ch[r] << 7) + cl[r]), dk[r], sacc[nt][mt][r]);
         }
       }
     }
 
-    // ---- online softmax (base 2) ----
-    float pr[NP][8];
+    // ---- online softmax (base 2, lazily rescaled reference max) ----
+    uint32_t pp[NP][4];  // p of the lane's 8 tokens as packed f16 pairs
 #pragma unroll
     for (int np = 0; np < NP; ++np) {
       float s[8];
@@ -264,37 +314,60 @@ struct Decoder {
         }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float mnew = fmaxf(mrun[np], tmax);
-      const float muse = mnew == -INFINITY ? 0.0f : mnew;
-      const float alpha = __builtin_amdgcn_exp2f(mrun[np] - muse);
+      const bool need = tmax > mref[np] + kTau;  // also true for the first visible tile
+      if (__any(need)) {
+        const float mnew = need ? tmax : mref[np];
+        const float alpha = !need ? 1.0f : (mref[np] == -INFINITY ? 0.0f
+                                                                  : __builtin_amdgcn_exp2f(mref[np] - mnew));
+        lrun[np] *= alpha;
+#pragma unroll
+        for (int m = 0; m < D / 16; ++m) oacc[np][m] *= alpha;
+        mref[np] = mnew;
+      }
+      const float muse = mref[np] == -INFINITY ? 0.0f : mref[np];
+      float pr[8];
       float lsum = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pr[np][e] = __builtin_amdgcn_exp2f(s[e] - muse);
-        lsum += pr[np][e];
+        pr[e] = __builtin_amdgcn_exp2f(s[e] - muse);
+        lsum += pr[e];
       }
-      lrun[np] = lrun[np] * alpha + lsum;
-      mrun[np] = mnew;
-      // alpha == 1 exactly unless this row's max moved; rescale only then
-      if (__any(alpha != 1.0f)) {
+      lrun[np] += lsum;
 #pragma unroll
-        for (int m = 0; m < D / 16; ++m) oacc[np][m] *= alpha;
+      for (int i = 0; i < 4; ++i) {
+        const v2h h2 = {(_Float16)pr[2 * i], (_Float16)pr[2 * i + 1]};
+        pp[np][i] = __builtin_bit_cast(uint32_t, h2);
       }
     }
 
-    // ---- PV ----
+    // ---- PV: B = p * d_v as packed f16 (one rounding of the exact product of
+    // the f16-rounded p and the stored f16 scale) ----
+    // Tokens past the sequence end may carry junk scales; zero them on the
+    // last tile so 0 * junk cannot turn into NaN.
+    const bool tail = t0 + kTile > len;
+    uint32_t smask[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
+    if (tail) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tk = t0 + (i < 2 ? 0 : 16) + 4 * lg + 2 * (i & 1);
+        smask[i] = (tk < len ? 0xffffu : 0u) | (tk + 1 < len ? 0xffff0000u : 0u);
+      }
+    }
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
-      const v4f dv0 = f16x4_to_f32(lds_load<uint2>(st + S::kVS + 2 * (blk * 32 + 4 * lg)));
-      const v4f dv1 = f16x4_to_f32(lds_load<uint2>(st + S::kVS + 2 * (blk * 32 + 16 + 4 * lg)));
+      // (ext-vector loads only: an LDS load of the uint4 struct type makes the
+      // compiler drain every in-flight copy before it)
+      const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
+      const uint32_t sc[4] = {(uint32_t)sv[0] & smask[0], (uint32_t)sv[1] & smask[1],
+                              (uint32_t)sv[2] & smask[2], (uint32_t)sv[3] & smask[3]};
       v8h pb[NP];
 #pragma unroll
       for (int np = 0; np < NP; ++np) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // masked tokens have p == 0 and may carry junk scales: keep them 0
-          pb[np][e] = (_Float16)(pr[np][e] > 0.0f ? pr[np][e] * dv0[e] : 0.0f);
-          pb[np][4 + e] = (_Float16)(pr[np][4 + e] > 0.0f ? pr[np][4 + e] * dv1[e] : 0.0f);
+        for (int i = 0; i < 4; ++i) {
+          const v2h prod = __builtin_bit_cast(v2h, pp[np][i]) * __builtin_bit_cast(v2h, sc[i]);
+          pb[np][2 * i] = prod[0];
+          pb[np][2 * i + 1] = prod[1];
         }
       }
 #pragma unroll
@@ -314,33 +387,66 @@ struct Decoder {
     }
   }
 
-  // Prefetch the next tile into `next`, wait for `cur`, compute `cur`.  The
-  // two stages are distinct restrict pointers so the compiler can see that
-  // the reads of `cur` do not depend on the copies into `next` and keeps the
-  // explicit vmcnt wait below instead of draining every copy.
-  __device__ __forceinline__ void step(int tile, const lds_u8 *__restrict__ cur,
-                                       lds_u8 *__restrict__ next) {
-    if (tile + 1 < n_tiles) {
-      issue(tile + 1, next);
-      // vmcnt <= kInstr: every copy into `cur` has landed
-      __builtin_amdgcn_s_waitcnt(kWaitBase | (S::kInstr & 0xf) | ((S::kInstr >> 4) << 14));
+  // vmcnt wait for the tile about to be computed when `ahead` later tiles'
+  // copies are still in flight (each tile is S::kInstr copies).
+  __device__ __forceinline__ static void wait_tiles_ahead(int ahead) {
+    constexpr int kI = ChunkPlan<D, kSmall>::kInstr;
+    if (ahead >= 2) {
+      constexpr int n = 2 * kI;
+      __builtin_amdgcn_s_waitcnt(kWaitBase | (n & 0xf) | ((n >> 4) << 14));
+    } else if (ahead == 1) {
+      constexpr int n = kI;
+      __builtin_amdgcn_s_waitcnt(kWaitBase | (n & 0xf) | ((n >> 4) << 14));
     } else {
       __builtin_amdgcn_s_waitcnt(kWaitBase);
     }
-    compute(tile, cur);
+  }
+
+  // Tile t: prefetch tile t+NS-1 into `fill`, wait for `cur`, compute it.
+  __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
+    if (t + NS - 1 < n_tiles) issue(t + NS - 1, fill);
+    const int ahead = min(n_tiles - 1 - t, NS - 1);
+    wait_tiles_ahead(ahead);
+    compute(t, cur);
+  }
+
+  // The whole tile loop.  The stages are distinct restrict pointers of this
+  // one function, so the compiler can prove that reading one stage does not
+  // depend on the copies still landing in the others and keeps the explicit
+  // vmcnt waits above instead of draining every copy.
+  __device__ __forceinline__ void run(lds_u8 *__restrict__ s0, lds_u8 *__restrict__ s1,
+                                      lds_u8 *__restrict__ s2) {
+    if (n_tiles > 0) issue(0, s0);
+    if constexpr (NS == 2) {
+      int t = 0;
+      for (; t + 1 < n_tiles; t += 2) {
+        step(t, s0, s1);
+        step(t + 1, s1, s0);
+      }
+      if (t < n_tiles) step(t, s0, s1);
+    } else {
+      if (n_tiles > 1) issue(1, s1);
+      int t = 0;
+      for (; t + 2 < n_tiles; t += 3) {
+        step(t, s0, s2);
+        step(t + 1, s1, s0);
+        step(t + 2, s2, s1);
+      }
+      if (t < n_tiles) step(t, s0, s2);
+      if (t + 1 < n_tiles) step(t + 1, s1, s0);
+    }
   }
 };
-
 #endif  // __HIP_DEVICE_COMPILE__
 
-template <int D, int NT, bool kSmall>
+template <int D, int NT, bool kSmall, int NS>
 __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using Dec = Decoder<D, NT, kSmall>;
+  using Dec = Decoder<D, NT, kSmall, NS>;
   using S = StageShape<D>;
   constexpr int NP = Dec::NP;
   constexpr int NC = Dec::NC;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kStages][S::kAlloc];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
 
   Dec dc(p);
   dc.lane = threadIdx.x;
@@ -359,11 +465,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
     return;
   }
   const int32_t len = p.seq_lens[seq];
-  if (len < 0 || len > p.bt_stride * g.page_tokens) {
-    if (lane == 0) atomicOr(p.fault, FAULT_BAD_POSITION);
-    return;
-  }
-  if (len > p.n_parts * p.part_tokens) {  // longer than max_seq_len promised
+  if (len < 0 || len > p.bt_stride * g.page_tokens || len > p.n_parts * p.part_tokens) {
     if (lane == 0) atomicOr(p.fault, FAULT_BAD_POSITION);
     return;
   }
@@ -462,7 +564,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
       if (t == nt) mul = qmul[t];
     dc.rmul[np] = mul;
     dc.rlim[np] = (row < R && nt < NT) ? len - p.q_len + row / q_per_kv + 1 : 0;
-    dc.mrun[np] = -INFINITY;
+    dc.mref[np] = -INFINITY;
     dc.lrun[np] = 0.0f;
 #pragma unroll
     for (int m = 0; m < D / 16; ++m) dc.oacc[np][m] = v4f{0.f, 0.f, 0.f, 0.f};
@@ -471,9 +573,9 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   make_plan<D, kSmall>(dc.plan, g, lane);
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
-  // The partition's page ids, one per lane (the host keeps part_tokens <=
-  // 64 * page_tokens); bad entries are reported and replaced by page 0 so
-  // every copy stays inside the pool.
+  // The partition's page ids, one per lane (partitions start on a page
+  // boundary and span at most 64 pages); bad entries are reported and
+  // replaced by page 0 so every copy stays inside the pool.
   dc.pg_first = tok0 / g.page_tokens;
   {
     const int32_t npg = tok_end > tok0 ? (tok_end - 1) / g.page_tokens - dc.pg_first + 1 : 0;
@@ -485,16 +587,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
     dc.pidv = pid;
   }
 
-  lds_u8 *s0 = (lds_u8 *)lds[0];
-  lds_u8 *s1 = (lds_u8 *)lds[1];
-  const int nt_total = dc.n_tiles;
-  if (nt_total > 0) dc.issue(0, s0);
-  int tile = 0;
-  for (; tile + 1 < nt_total; tile += 2) {
-    dc.step(tile, s0, s1);
-    dc.step(tile + 1, s1, s0);
-  }
-  if (tile < nt_total) dc.step(tile, s0, s1);
+  dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
 
   // ---- epilogue ---------------------------------------------------------------
 #pragma unroll
@@ -527,13 +620,16 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
 #pragma unroll
       for (int m = 0; m < D / 16; ++m)
         *reinterpret_cast<v4f *>(p.ws_o + prow * D + 16 * m + 4 * lg) = dc.oacc[np][m];
-      if (lg == 0) *reinterpret_cast<float2 *>(p.ws_ml + 2 * prow) = float2{dc.mrun[np], l};
+      if (lg == 0) *reinterpret_cast<float2 *>(p.ws_ml + 2 * prow) = float2{dc.mref[np], l};
     }
   }
+
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-// One 256-thread block per (batch entry, row); thread = dimension.
+// One 256-thread block per (batch entry, row); thread = dimension.  Partials
+// are read once: (m, l) of every partition first (at most 64 in registers),
+// then the o vectors with all loads of a group in flight together.
 __global__ __launch_bounds__(256) void combine_kernel(CombineLaunch c) {
   const int row = blockIdx.x;
   const int b = blockIdx.y;
@@ -542,14 +638,30 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineLaunch c) {
   const int32_t len = (seq >= 0 && seq < c.n_seqs) ? c.seq_lens[seq] : 0;
   const int32_t np = len > 0 ? min(c.n_parts, (len + c.part_tokens - 1) / c.part_tokens) : 0;
   const int64_t prow = ((int64_t)b * c.rows + row) * c.n_parts;
+  const float2 *ml = reinterpret_cast<const float2 *>(c.ml) + prow;
   float M = -INFINITY;
-  for (int i = 0; i < np; ++i) M = fmaxf(M, c.ml[2 * (prow + i)]);
+  for (int i = 0; i < np; ++i) M = fmaxf(M, ml[i].x);
   float L = 0.0f, O = 0.0f;
-  if (M != -INFINITY) {
-    for (int i = 0; i < np; ++i) {
-      const float w = __builtin_amdgcn_exp2f(c.ml[2 * (prow + i)] - M);
-      L += c.ml[2 * (prow + i) + 1] * w;
-      if (d < c.head_dim) O += c.o[(prow + i) * c.head_dim + d] * w;
+  if (M != -INFINITY && d < c.head_dim) {
+    const float *o = c.o + prow * c.head_dim + d;
+    int i = 0;
+    for (; i + 8 <= np; i += 8) {
+      float w[8], ov[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ov[k] = o[(int64_t)(i + k) * c.head_dim];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float2 v = ml[i + k];
+        w[k] = __builtin_amdgcn_exp2f(v.x - M);
+        L += v.y * w[k];
+        O += ov[k] * w[k];
+      }
+    }
+    for (; i < np; ++i) {
+      const float2 v = ml[i];
+      const float w = __builtin_amdgcn_exp2f(v.x - M);
+      L += v.y * w;
+      O += o[(int64_t)i * c.head_dim] * w;
     }
   }
   if (d >= c.head_dim) return;
@@ -559,14 +671,21 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineLaunch c) {
   else static_cast<float *>(c.out)[oi] = r;
 }
 
-template <int D, int NT>
+template <int D, int NT, int NS>
 hipError_t launch_decode_t(const DecodeLaunch &d, hipStream_t s) {
   dim3 grid((unsigned)d.n_parts, (unsigned)d.batch, (unsigned)d.g.kv_heads);
   if (d.g.page_tokens < kTile)
-    hipLaunchKernelGGL((decode_kernel<D, NT, true>), grid, dim3(64), 0, s, d);
+    hipLaunchKernelGGL((decode_kernel<D, NT, true, NS>), grid, dim3(64), 0, s, d);
   else
-    hipLaunchKernelGGL((decode_kernel<D, NT, false>), grid, dim3(64), 0, s, d);
+    hipLaunchKernelGGL((decode_kernel<D, NT, false, NS>), grid, dim3(64), 0, s, d);
   return hipGetLastError();
+}
+
+template <int D, int NS>
+hipError_t launch_decode_d(const DecodeLaunch &d, int NT, hipStream_t s) {
+  if (NT == 1) return launch_decode_t<D, 1, NS>(d, s);
+  if (NT == 2) return launch_decode_t<D, 2, NS>(d, s);
+  return launch_decode_t<D, 4, NS>(d, s);
 }
 
 }  // namespace
@@ -575,14 +694,10 @@ hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s) {
   if (d.batch == 0 || d.n_parts == 0) return hipSuccess;
   const int R = d.q_len * (d.q_heads / d.g.kv_heads);
   const int NT = R <= 8 ? 1 : (R <= 16 ? 2 : 4);
-  if (d.g.head_dim == 256) {
-    if (NT == 1) return launch_decode_t<256, 1>(d, s);
-    if (NT == 2) return launch_decode_t<256, 2>(d, s);
-    return launch_decode_t<256, 4>(d, s);
-  }
-  if (NT == 1) return launch_decode_t<128, 1>(d, s);
-  if (NT == 2) return launch_decode_t<128, 2>(d, s);
-  return launch_decode_t<128, 4>(d, s);
+  const bool three = d.stages != 2;
+  if (d.g.head_dim == 256)
+    return three ? launch_decode_d<256, 3>(d, NT, s) : launch_decode_d<256, 2>(d, NT, s);
+  return three ? launch_decode_d<128, 3>(d, NT, s) : launch_decode_d<128, 2>(d, NT, s);
 }
 
 hipError_t launch_combine(const CombineLaunch &c, hipStream_t s) {

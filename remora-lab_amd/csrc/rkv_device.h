@@ -15,10 +15,14 @@ namespace rkv {
 // A page holds page_tokens token slots for every kv head, K then V:
 //   page   = [kv_head][kind K|V][region]
 //   region = codes (page_tokens*D bytes) then scales (page_tokens*D/32 f16)
-//   K codes : [slot][dim]                 -- the reference row order
-//   V codes : [slot/TT][dim][slot%TT]     -- dim-major inside 32-slot tiles
-//   scales  : [slot/TT][block][slot%TT]   -- K and V alike
-// with TT = min(32, page_tokens).  The bytes of one reference row
+//   K codes : [slot][dim]                     -- the reference row order
+//   V codes : [slot/TT][dim][slot%TT]         -- dim-major inside 32-slot tiles
+//   scales  : [slot/TT][block][sigma(slot%TT)] -- K and V alike
+// with TT = min(32, page_tokens).  Inside a 32-slot tile the scales are kept
+// in the order the decode kernel's lanes consume them: slot t = 16*m + 4*g + r
+// (m < 2, g < 4, r < 4) sits at position sigma(t) = 8*g + 4*m + r, so one
+// 16-byte read gives a lane the 8 scales of its tokens; 16-slot tiles keep
+// slot order.  The bytes of one reference row
 // (har/crates/har-serve/src/attention.rs:17-21: per 32-value block an LE f16
 // scale then 32 int8 codes) are a fixed permutation of these; rkv_gather_q8
 // applies the inverse.  Why: a 32-token tile of K codes, of V codes and of
@@ -54,13 +58,18 @@ __host__ __device__ inline uint32_t code_offset(const Geo &g, int32_t kind, int3
   const uint32_t TT = (uint32_t)tile_tokens(g.page_tokens);
   return ((uint32_t)slot / TT) * D * TT + (uint32_t)dim * TT + (uint32_t)slot % TT;
 }
+// position of tile slot t inside a 32-slot scale run
+__host__ __device__ inline uint32_t scale_pos32(uint32_t t) {
+  return 8u * ((t >> 2) & 3u) + 4u * (t >> 4) + (t & 3u);
+}
 // byte offset of the f16 scale of (slot, block) inside a region
 __host__ __device__ inline uint32_t scale_offset(const Geo &g, int32_t slot, int32_t block) {
   const uint32_t D = (uint32_t)g.head_dim;
   const uint32_t TT = (uint32_t)tile_tokens(g.page_tokens);
+  const uint32_t t = (uint32_t)slot % TT;
   return (uint32_t)g.page_tokens * D +
          2u * (((uint32_t)slot / TT) * (D / 32u) * TT + (uint32_t)block * TT +
-               (uint32_t)slot % TT);
+               (TT == 32u ? scale_pos32(t) : t));
 }
 
 // Device-side fault word bits (read back by rkv_ctx_sync).

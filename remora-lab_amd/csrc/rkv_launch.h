@@ -57,9 +57,24 @@ struct DecodeLaunch {
   float *ws_ml;
   float *ws_o;
   int32_t *fault;
+  int32_t stages;  // LDS ring depth: 2 or 3 (tiles in flight = stages - 1)
 };
 // rows per kv head = q_len * q_heads / kv_heads must be <= 32
 hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s);
+
+// Decode workgroups (one wave each) resident per CU, the lesser of
+//  - LDS: `stages` tile stages of 68*head_dim bytes, padded to 1 KiB, out of
+//    the CU's 160 KiB;
+//  - registers: head_dim 256, or more than 16 rows per kv head, takes more
+//    than half of a SIMD's 512 VGPR+AGPR per lane (one wave per SIMD);
+//    smaller shapes fit two waves per SIMD.
+constexpr int decode_wgs_per_cu(int head_dim, int rows, int stages) {
+  const int stage = (68 * head_dim / 16 + 63) / 64 * 1024;
+  const int by_lds = 160 * 1024 / (stages * stage);
+  const int by_regs = (head_dim == 256 || rows > 16) ? 4 : 8;
+  return by_lds < by_regs ? by_lds : by_regs;
+}
+constexpr int kComputeUnits = 256;  // MI355X (gfx950)
 
 struct CombineLaunch {
   const float *ml;

@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -313,13 +314,20 @@ rkv_status rkv_alloc_export(const rkv_alloc *a, int32_t *tables, int32_t *lens) 
 // ---------------------------------------------------------------------------
 namespace {
 
+int32_t decode_stages();
+
 int32_t auto_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *a) {
-  // Aim for >= ~2048 work units over the 256 CUs, in tiles of 32 tokens,
-  // never more than 64 pages per partition (the kernel keeps one page id
-  // per lane).
+  // One full round of resident workgroups: split each sequence into as many
+  // partitions as fit beside the other (batch entry, kv head) pairs, so no
+  // CU waits on a second, partial round.  Partitions are whole pages and
+  // 32-token tiles, at least 256 tokens, at most 64 pages (the kernel keeps
+  // one page id per lane).
   const int64_t max_len = std::max<int64_t>(a->max_seq_len, 1);
-  const int64_t units_per_part = (int64_t)a->batch * g->kv_heads;
-  int64_t parts = (2048 + units_per_part - 1) / std::max<int64_t>(units_per_part, 1);
+  const int64_t pairs = std::max<int64_t>((int64_t)a->batch * g->kv_heads, 1);
+  const int32_t rows = a->q_len * (a->q_heads / std::max(g->kv_heads, 1));
+  const int64_t slots = (int64_t)rkv::kComputeUnits *
+                        rkv::decode_wgs_per_cu(g->head_dim, rows, decode_stages());
+  const int64_t parts = std::max<int64_t>(1, slots / pairs);
   int64_t pt = (max_len + parts - 1) / parts;
   const int64_t unit = std::max<int32_t>(32, g->page_tokens);
   pt = std::max<int64_t>(pt, 256);
@@ -359,10 +367,25 @@ rkv_status check_decode(const rkv_kv_geometry *g, const rkv_decode_args *a, cons
   return RKV_OK;
 }
 
+// LDS ring depth of the decode kernel.  2 stages (one tile in flight per
+// workgroup, four workgroups per CU) is the default: measured at the
+// headline shape it beats 3 stages (two tiles in flight, but only three
+// workgroups per CU, so one SIMD idles).  RKV_DECODE_STAGES=3 selects the
+// deeper ring for measurement.
+int32_t decode_stages() {
+  static const int32_t v = [] {
+    const char *e = std::getenv("RKV_DECODE_STAGES");
+    return (e && std::atoi(e) == 3) ? 3 : 2;
+  }();
+  return v;
+}
+
 int32_t parts_of(const rkv_decode_args *a, int32_t pt) {
   return std::max<int32_t>(1, (a->max_seq_len + pt - 1) / pt);
 }
 
+// Workspace of a multi-partition decode: partials (m, l) and o of every
+// (row, partition).
 size_t ws_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a, int32_t pt) {
   const int32_t np = parts_of(a, pt);
   if (np == 1) return 0;
@@ -392,6 +415,7 @@ rkv::DecodeLaunch make_decode(rkv_ctx *ctx, const rkv_kv_geometry *g, const void
   d.out = a->out;
   d.out_bf16 = a->out_dtype == RKV_BF16;
   d.fault = ctx->d_fault;
+  d.stages = decode_stages();
   return d;
 }
 
