@@ -228,7 +228,7 @@ def main() -> int:
                       "event_step": round(1e6 * sum(t_step) / len(t_step), 2)},
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
-        "roofline": {"bound": "hbm", "kernel": "decode_kernel<256,1,false>",
+        "roofline": {"bound": "hbm", "kernel": "decode_kernel<256,1,false,2>",
                      "achieved": round(dec_bytes / dec_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(), "algorithmic_bytes_per_launch": dec_bytes},
