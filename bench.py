@@ -194,10 +194,11 @@ def main() -> int:
     bt_bytes = B * pages_per_seq * 4
     app_bytes = B * Hkv * 2 * (D * 2 + row)
     step_bytes = kv_bytes + q_bytes + out_bytes + bt_bytes + app_bytes
+    # split-K partials are implementation overhead, reported beside the
+    # algorithmic figure and not in it
     partial_bytes = B * rows * n_parts * (D + 2) * 4
-    # the decode kernel reads K/V, q and the block tables and writes the
-    # partials (or `out` when one partition covers the sequence)
-    dec_bytes = kv_bytes + q_bytes + bt_bytes + (partial_bytes if n_parts > 1 else out_bytes)
+    # the decode kernel's share of the step: K/V, q, block tables, out
+    dec_bytes = kv_bytes + q_bytes + bt_bytes + out_bytes
     flops = 4 * D * Hq * B * L
 
     value = step_bytes / step_s / 1e9

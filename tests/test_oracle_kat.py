@@ -110,6 +110,34 @@ def test_f16_matches_numpy_rtne(rko):
     assert np.array_equal(got, want)
 
 
+def test_f16_decoders_exhaustive(rko):
+    """Both binary16 decoders (f16.rs:4-25, q4k.rs:22-50) against numpy's
+    float16 -> float32 widening over all 65536 bit patterns."""
+    L = rko.lib()
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    a = np.array([L.rko_f16_to_f32(int(b)) for b in bits], np.float32)
+    h = np.array([L.rko_f16_to_f32_harserve(int(b) & 0xFF, int(b) >> 8) for b in bits], np.float32)
+    nan = np.isnan(want)
+    for got in (a, h):
+        assert np.array_equal(np.isnan(got), nan)
+        assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_bf16_matches_torch(rko):
+    """The bf16 rounding used to make bf16 test inputs is torch's (RTNE)."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(4)
+    bits = rng.integers(0, 2 ** 32, 50000, dtype=np.uint64).astype(np.uint32)
+    x = bits.view(np.float32)
+    x = x[~np.isnan(x)]
+    got = rko.f32_to_bf16(x)
+    want = torch.from_numpy(x.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got.reshape(-1), want)
+    L = rko.lib()
+    assert all(L.rko_f32_to_bf16(float(v)) == w for v, w in zip(x[:5000], want[:5000]))
+
+
 def test_harserve_f16_roundtrip(rko):
     """attention.rs:289-296: |v - f16(v)| < 1e-3 for the listed values."""
     L = rko.lib()
