@@ -8,7 +8,9 @@ bf16 query ~ N(0,1); softmax scale 1/16; f32 output; seed 0.
 
 One step = append one K/V row per sequence (position L-1, the same slot every
 step, so every step is the same work) + split-K decode + LSE combine, all on
-one stream.  Inputs are resident in HBM before the timed region.
+one stream: two launches, the decode launch quantizing and writing the new
+rows itself before it reads them (--append-launch: a separate append launch
+first).  Inputs are resident in HBM before the timed region.
 
 Printed: ONE JSON line (rank 0) with the whole-step algorithmic HBM rate
 (`value`, GB/s), us/step, the decode kernel's roofline figures measured with
@@ -55,6 +57,9 @@ def parse():
     ap.add_argument("--head-dim", type=int, default=256)
     ap.add_argument("--page-size", type=int, default=64)
     ap.add_argument("--partition-tokens", type=int, default=0)
+    ap.add_argument("--append-launch", action="store_true",
+                    help="append the step's rows with a separate rkv_pool_append launch instead "
+                         "of inside the decode launch")
     ap.add_argument("--cpu-sample-seqs", type=int, default=4,
                     help="sequences of the oracle CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=0)
@@ -139,15 +144,23 @@ def main() -> int:
     bt_p = pool.block_tables_ptr()
     lens_p = pool.seq_lens_ptr()
 
+    # this step's new K/V rows, appended by the decode launch itself (the
+    # default) or by a separate rkv_pool_append launch (--append-launch)
+    app = rkv.append_args(seq_ids, positions, k_new, v_new)
+    a = rkv.decode_args(q, out, seq_ids, scale, L, partition_tokens=args.partition_tokens,
+                        append=None if args.append_launch else app)
+    fused = not args.append_launch
+
     def step(ev=None):
-        # rkv_pool_append, then the two kernels rkv_pool_decode chains
-        # (split-K decode, log-sum-exp combine), called through their
-        # kernel-level entry points so events can bracket each kernel
+        # [append launch], then the two kernels rkv_pool_decode chains (split-K
+        # decode, log-sum-exp combine), called through their kernel-level entry
+        # points so events can bracket each kernel on the launch stream
         if ev is not None:
             ev[0].record(stream)
-        pool.append(0, seq_ids, positions, k_new, v_new, stream=stream)
-        if ev is not None:
-            ev[1].record(stream)
+        if not fused:
+            pool.append(0, seq_ids, positions, k_new, v_new, stream=stream)
+            if ev is not None:
+                ev[1].record(stream)
         if n_parts > 1:
             rkv.check(lib.rkv_decode_q8_partials(ctx.h, C.byref(g), C.c_void_p(pages_p),
                                                  C.c_void_p(bt_p), pages_per_seq,
@@ -179,9 +192,10 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ctx.sync()
+    dec_from = 0 if fused else 1  # the decode launch starts after the append launch
     t_step = [evs[i][0].elapsed_time(evs[i][3]) * 1e-3 for i in range(args.steps)]
-    t_app = [evs[i][0].elapsed_time(evs[i][1]) * 1e-3 for i in range(args.steps)]
-    t_dec = [evs[i][1].elapsed_time(evs[i][2]) * 1e-3 for i in range(args.steps)]
+    t_app = [0.0 if fused else evs[i][0].elapsed_time(evs[i][1]) * 1e-3 for i in range(args.steps)]
+    t_dec = [evs[i][dec_from].elapsed_time(evs[i][2]) * 1e-3 for i in range(args.steps)]
     t_cmb = [evs[i][2].elapsed_time(evs[i][3]) * 1e-3 for i in range(args.steps)]
     step_s = wall / args.steps  # whole-job rate over the timed region
     dec_s = sum(t_dec) / len(t_dec)
@@ -197,8 +211,9 @@ def main() -> int:
     # split-K partials are implementation overhead, reported beside the
     # algorithmic figure and not in it
     partial_bytes = B * rows * n_parts * (D + 2) * 4
-    # the decode kernel's share of the step: K/V, q, block tables, out
-    dec_bytes = kv_bytes + q_bytes + bt_bytes + out_bytes
+    # the decode kernel's share of the step: K/V, q, block tables, out, and
+    # the appended rows when it appends them itself
+    dec_bytes = kv_bytes + q_bytes + bt_bytes + out_bytes + (app_bytes if fused else 0)
     flops = 4 * D * Hq * B * L
 
     value = step_bytes / step_s / 1e9
@@ -219,7 +234,8 @@ def main() -> int:
                                f"D={D}, page={PT}, 10% pool slack, bf16 q, f32 out, scale 1/{int(math.sqrt(D))}",
                    "batch": B, "ctx": L, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D,
                    "page_tokens": PT, "partition_tokens": part, "partitions": n_parts,
-                   "pool_pages": num_pages},
+                   "pool_pages": num_pages,
+                   "append": "separate launch" if args.append_launch else "inside the decode launch"},
         "us_per_step": round(step_s * 1e6, 2),
         "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "algorithmic_bytes_per_step": step_bytes,

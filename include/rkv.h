@@ -147,6 +147,16 @@ typedef struct rkv_decode_args {
                                rkv_decode_workspace_bytes (may be NULL when one
                                partition covers every sequence) */
   size_t workspace_bytes;
+  const rkv_append_args *append; /* optional (NULL = none): this step's K/V rows,
+                               appended by the decode launch itself before it
+                               attends over them.  n_rows = batch*q_len; row
+                               b*q_len+j belongs to seq_ids[b] (else fault bit
+                               4) at a position < its seq_lens entry (else
+                               fault bit 2).  `pages` must then be writable.
+                               Same bytes as rkv_append_q8 of the same rows,
+                               one launch fewer per step (the reference step
+                               quantizes, then dispatches the decode:
+                               har-serve-vulkan-attn-smoke.rs:62-69, 149-161). */
 } rkv_decode_args;
 
 /* ---- kernel-level entry points (explicit device pointers) -----------------

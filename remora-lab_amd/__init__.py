@@ -62,7 +62,8 @@ class DecodeArgs(C.Structure):
     _fields_ = [("batch", C.c_int32), ("seq_ids", P), ("q", P), ("q_dtype", C.c_int32),
                 ("q_len", C.c_int32), ("q_heads", C.c_int32), ("scale", C.c_float),
                 ("out", P), ("out_dtype", C.c_int32), ("partition_tokens", C.c_int32),
-                ("max_seq_len", C.c_int32), ("workspace", P), ("workspace_bytes", C.c_size_t)]
+                ("max_seq_len", C.c_int32), ("workspace", P), ("workspace_bytes", C.c_size_t),
+                ("append", C.POINTER(AppendArgs))]
 
 
 class FlashDecodeParams(C.Structure):
@@ -278,8 +279,20 @@ def append_q8(ctx: Ctx, g: Geometry, pages, block_tables, seq_ids, positions, k_
                               n_seqs, C.byref(a), _stream(stream)))
 
 
+def append_args(seq_ids, positions, k_src, v_src, rule=Q8_CANONICAL) -> AppendArgs:
+    """Rows [n][kv_heads][head_dim] (f32 or bf16) for rkv_append_q8 or for the
+    `append` of a decode."""
+    import torch
+    a = AppendArgs(seq_ids.numel(), _ptr(seq_ids), _ptr(positions), _ptr(k_src), _ptr(v_src),
+                   BF16 if k_src.dtype == torch.bfloat16 else F32, rule)
+    a._refs = (seq_ids, positions, k_src, v_src)
+    return a
+
+
 def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0,
-                workspace=None) -> DecodeArgs:
+                workspace=None, append: AppendArgs | None = None) -> DecodeArgs:
+    """`append` (optional): rows [batch*q_len] the decode launch appends
+    before attending over them."""
     import torch
     B = seq_ids.numel()
     q_heads = q.shape[-2]
@@ -287,8 +300,9 @@ def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0
                    q_len, q_heads, scale, _ptr(out),
                    BF16 if out.dtype == torch.bfloat16 else F32, partition_tokens,
                    max_seq_len, _ptr(workspace),
-                   0 if workspace is None else workspace.numel() * workspace.element_size())
-    a._refs = (q, out, seq_ids, workspace)  # the struct holds raw device pointers
+                   0 if workspace is None else workspace.numel() * workspace.element_size(),
+                   C.pointer(append) if append is not None else None)
+    a._refs = (q, out, seq_ids, workspace, append)  # the struct holds raw pointers
     return a
 
 

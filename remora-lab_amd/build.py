@@ -15,7 +15,13 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "librkv.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-SOURCES = ["rkv_append.hip", "rkv_decode.hip", "rkv_runtime.cpp"]
+SOURCES = ["rkv_append.hip", "rkv_decode.hip", "rkv_decode_rows32.hip", "rkv_runtime.cpp"]
+
+# Per-file extra flags.  rkv_decode.hip: MFMA destinations and accumulators
+# in VGPRs (no AGPR<->VGPR copies around the VALU work on them); the 32-row
+# variant in rkv_decode_rows32.hip stays on the default allocation (the
+# option crashes the compiler on it).
+EXTRA = {"rkv_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 # -packed-fp32-ops off: no v_pk_*_f32 are generated (unreliable on this pool).
 # f32 division and sqrt stay correctly rounded and f32 denormals are kept, so
@@ -42,7 +48,7 @@ def _hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.splitext(src)[0] + ".o")
-    cmd = [_hipcc(), *HIPFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [_hipcc(), *HIPFLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     if src.endswith(".hip"):
         cmd[1:1] = ["-x", "hip"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -2,14 +2,9 @@
 // bit-exact gather/import between pages and reference rows, and a batch
 // f16 encoder (gfx950).
 //
-// Quantization rules (bit-exact with the CPU reference):
-//   canonical (har/crates/r4kv/src/quant.rs:45-90): amax = max|v| over the
-//     32-value group, d = amax/127 (f32, IEEE division), inv = 1/d,
-//     q = clamp(round_half_away(v*inv), -127, 127), scale = f16_rtne(d);
-//   har-serve (har/crates/har-serve/src/attention.rs:25-42): same d,
-//     q = clamp(round_half_away(v/d)), scale = attention.rs's f16 encoder.
-// hipcc keeps f32 division correctly rounded (flag set by the build) and
-// this file has no a*b+c patterns, so contraction cannot change a result.
+// Quantization rules (bit-exact with the CPU reference): q8_quantize_lane
+// in rkv_device.h -- canonical (har/crates/r4kv/src/quant.rs:45-90) or
+// har-serve (har/crates/har-serve/src/attention.rs:25-42).
 #include "rkv_launch.h"
 
 namespace rkv {
@@ -39,48 +34,11 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
   if (live) {
     const uint64_t off =
         ((uint64_t)row * (uint64_t)a.g.kv_heads + (uint64_t)kvh) * (uint64_t)D + (uint64_t)(b * 32 + sub * 4);
-    const void *src = kind == 0 ? a.k_src : a.v_src;
-    if (a.src_bf16) {
-      const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(src) + off);
-      v[0] = bf16_bits_to_f32((uint16_t)(w.x & 0xffffu));
-      v[1] = bf16_bits_to_f32((uint16_t)(w.x >> 16));
-      v[2] = bf16_bits_to_f32((uint16_t)(w.y & 0xffffu));
-      v[3] = bf16_bits_to_f32((uint16_t)(w.y >> 16));
-    } else {
-      const float4 w = *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + off);
-      v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
-    }
+    load_src4(kind == 0 ? a.k_src : a.v_src, off, a.src_bf16 != 0, v);
   }
-  // amax ignores NaN (quant.rs:49-55 compares `a > amax`; attention.rs:29
-  // uses f32::max) -- both equal this.
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float x = fabsf(v[i]);
-    amax = x > amax ? x : amax;
-  }
-  amax = fmaxf(amax, __shfl_xor(amax, 1));
-  amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
-  if (!live) return;
-
-  const float d = amax == 0.0f ? 0.0f : amax / 127.0f;
-  uint32_t codes = 0;
   uint16_t scale;
-  if (a.rule == 0) {
-    const float inv = d == 0.0f ? 0.0f : 1.0f / d;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      codes |= ((uint32_t)(uint8_t)(int8_t)q8_code(roundf(v[i] * inv))) << (8 * i);
-    scale = f16_rtne(d);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int32_t q = d == 0.0f ? 0 : q8_code(roundf(v[i] / d));
-      codes |= ((uint32_t)(uint8_t)(int8_t)q) << (8 * i);
-    }
-    scale = f16_harserve(d);
-  }
+  const uint32_t codes = q8_quantize_lane(v, a.rule, scale);
+  if (!live) return;
 
   const int32_t seq = a.seq_ids[row];
   const int32_t pos = a.positions[row];
@@ -98,15 +56,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
     return;
   }
   const int32_t slot = pos % a.g.page_tokens;
-  uint8_t *region = a.pages + region_base(a.g, page, kvh, kind);
-  const int32_t dim0 = b * 32 + sub * 4;
-  if (kind == 0) {
-    *reinterpret_cast<uint32_t *>(region + code_offset(a.g, 0, slot, dim0)) = codes;
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) region[code_offset(a.g, 1, slot, dim0 + i)] = (uint8_t)(codes >> (8 * i));
-  }
-  if (sub == 0) *reinterpret_cast<uint16_t *>(region + scale_offset(a.g, slot, b)) = scale;
+  store_q8_lane(a.g, a.pages + region_base(a.g, page, kvh, kind), kind, slot, b, sub, codes, scale);
 }
 
 // One thread per (kv_head, position, block): 34 reference-row bytes.

@@ -157,4 +157,73 @@ __device__ inline int32_t q8_code(float r) {
   return (int32_t)r;
 }
 
+// ---------------------------------------------------------------------------
+// Q8_0 quantization of one 32-value block by 8 consecutive lanes; lane `sub`
+// of the group owns values 4*sub..4*sub+3.  Every lane of the wave must make
+// the call (the group max is three xor-shuffles).
+//   canonical (har/crates/r4kv/src/quant.rs:45-90): d = amax/127, inv = 1/d,
+//     q = clamp(round_half_away(v*inv)), scale = f16_rtne(d);
+//   har-serve (har/crates/har-serve/src/attention.rs:25-42): same d,
+//     q = clamp(round_half_away(v/d)), scale = f16_harserve(d).
+// amax ignores NaN (quant.rs:49-55 compares `a > amax`; attention.rs:29
+// uses f32::max).  f32 division is IEEE (the build keeps it correctly
+// rounded) and nothing here contracts into an FMA.
+// ---------------------------------------------------------------------------
+__device__ inline uint32_t q8_quantize_lane(const float v[4], int32_t rule, uint16_t &scale) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float x = fabsf(v[i]);
+    amax = x > amax ? x : amax;
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 1));
+  amax = fmaxf(amax, __shfl_xor(amax, 2));
+  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  const float d = amax == 0.0f ? 0.0f : amax / 127.0f;
+  uint32_t codes = 0;
+  if (rule == 0) {
+    const float inv = d == 0.0f ? 0.0f : 1.0f / d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      codes |= ((uint32_t)(uint8_t)(int8_t)q8_code(roundf(v[i] * inv))) << (8 * i);
+    scale = f16_rtne(d);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int32_t q = d == 0.0f ? 0 : q8_code(roundf(v[i] / d));
+      codes |= ((uint32_t)(uint8_t)(int8_t)q) << (8 * i);
+    }
+    scale = f16_harserve(d);
+  }
+  return codes;
+}
+
+// Four consecutive source values (f32 or bf16) starting at element `off`.
+__device__ inline void load_src4(const void *src, uint64_t off, bool bf16, float v[4]) {
+  if (bf16) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(src) + off);
+    v[0] = bf16_bits_to_f32((uint16_t)(w.x & 0xffffu));
+    v[1] = bf16_bits_to_f32((uint16_t)(w.x >> 16));
+    v[2] = bf16_bits_to_f32((uint16_t)(w.y & 0xffffu));
+    v[3] = bf16_bits_to_f32((uint16_t)(w.y >> 16));
+  } else {
+    const float4 w = *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + off);
+    v[0] = w.x; v[1] = w.y; v[2] = w.z; v[3] = w.w;
+  }
+}
+
+// Store lane `sub`'s 4 codes of block `blk` of token `slot` into a K or V
+// region, and (lane 0 of the group) the block's scale.
+__device__ inline void store_q8_lane(const Geo &g, uint8_t *region, int32_t kind, int32_t slot,
+                                     int32_t blk, int32_t sub, uint32_t codes, uint16_t scale) {
+  const int32_t dim0 = blk * 32 + sub * 4;
+  if (kind == 0) {
+    *reinterpret_cast<uint32_t *>(region + code_offset(g, 0, slot, dim0)) = codes;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) region[code_offset(g, 1, slot, dim0 + i)] = (uint8_t)(codes >> (8 * i));
+  }
+  if (sub == 0) *reinterpret_cast<uint16_t *>(region + scale_offset(g, slot, blk)) = scale;
+}
+
 }  // namespace rkv

@@ -58,9 +58,22 @@ struct DecodeLaunch {
   float *ws_o;
   int32_t *fault;
   int32_t stages;  // LDS ring depth: 2 or 3 (tiles in flight = stages - 1)
+  // Optional append (app_k == nullptr: none): row b*q_len + j of app_k/app_v
+  // ([rows][kv_heads][head_dim]) goes to position app_pos[row] of sequence
+  // seq_ids[b] before the decode reads it; the workgroup whose partition
+  // holds that position writes it.
+  uint8_t *pages_w;  // == pages, writable
+  const int32_t *app_seq_ids;
+  const int32_t *app_pos;
+  const void *app_k;
+  const void *app_v;
+  int32_t app_bf16;
+  int32_t app_rule;
 };
 // rows per kv head = q_len * q_heads / kv_heads must be <= 32
 hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s);
+// the 17..32-row instantiations (own translation unit)
+hipError_t launch_decode_rows32(const DecodeLaunch &d, hipStream_t s);
 
 // Decode workgroups (one wave each) resident per CU, the lesser of
 //  - LDS: `stages` tile stages of 68*head_dim bytes, padded to 1 KiB, out of

@@ -364,6 +364,17 @@ rkv_status check_decode(const rkv_kv_geometry *g, const rkv_decode_args *a, cons
   if (a->batch > 0 && (!a->seq_ids || !a->q || !a->out))
     return fail(RKV_ERR_INVALID_ARG, op, "NULL seq_ids/q/out");
   if (a->batch > 65535) return fail(RKV_ERR_INVALID_ARG, op, "batch=%d > 65535", a->batch);
+  if (const rkv_append_args *ap = a->append) {
+    if (ap->n_rows != a->batch * a->q_len)
+      return fail(RKV_ERR_INVALID_ARG, op, "append n_rows=%d != batch*q_len=%d", ap->n_rows,
+                  a->batch * a->q_len);
+    if (ap->src_dtype != RKV_F32 && ap->src_dtype != RKV_BF16)
+      return fail(RKV_ERR_UNSUPPORTED, op, "append src_dtype=%d", ap->src_dtype);
+    if (ap->rule != RKV_Q8_CANONICAL && ap->rule != RKV_Q8_HARSERVE)
+      return fail(RKV_ERR_INVALID_ARG, op, "append rule=%d", ap->rule);
+    if (ap->n_rows > 0 && (!ap->seq_ids || !ap->positions || !ap->k_src || !ap->v_src))
+      return fail(RKV_ERR_INVALID_ARG, op, "NULL append seq_ids/positions/k_src/v_src");
+  }
   return RKV_OK;
 }
 
@@ -416,6 +427,15 @@ rkv::DecodeLaunch make_decode(rkv_ctx *ctx, const rkv_kv_geometry *g, const void
   d.out_bf16 = a->out_dtype == RKV_BF16;
   d.fault = ctx->d_fault;
   d.stages = decode_stages();
+  if (const rkv_append_args *ap = a->append; ap && ap->n_rows > 0) {
+    d.pages_w = static_cast<uint8_t *>(const_cast<void *>(pages));
+    d.app_seq_ids = ap->seq_ids;
+    d.app_pos = ap->positions;
+    d.app_k = ap->k_src;
+    d.app_v = ap->v_src;
+    d.app_bf16 = ap->src_dtype == RKV_BF16;
+    d.app_rule = ap->rule;
+  }
   return d;
 }
 

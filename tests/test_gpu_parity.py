@@ -526,6 +526,92 @@ def test_workspace_reuse_repeated_calls(rkv, rko, ctx):
         assert_close(got, want, what=f"call {call}")
 
 
+def _last_rows(sc, b, q_len):
+    """The scene's source rows of sequence b at positions len-q_len .. len-1."""
+    start = int(np.sum(sc.lens[:b])) + int(sc.lens[b]) - q_len
+    return sc.k[start:start + q_len], sc.v[start:start + q_len]
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,PT,lens,q_len,part,rule", [
+    (16, 2, 256, 64, [3000, 1000, 64, 2500, 1], 1, 512, 0),
+    (16, 4, 128, 16, [514, 300, 4, 1030], 4, 512, 0),
+    (8, 2, 256, 32, [2049, 33, 40], 2, 1024, 1),
+])
+def test_append_in_decode(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, rule):
+    """The decode launch's own append (rkv_decode_args.append) writes the same
+    bytes as rkv_append_q8 -- also for draft rows that straddle a partition
+    boundary and for rows in a partition's first tile -- and its output equals
+    append-then-decode bit for bit (and the oracle within tolerance)."""
+    torch = _torch()
+    print(f"append-in-decode Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens} q_len={q_len}", flush=True)
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=40 + D + q_len, src_bf16=True, rule=rule)
+    B = len(lens)
+    # the pages the fused path starts from hold junk at the rows it appends
+    fused = sc.pages_d.clone()
+    rng = np.random.default_rng(8)
+    sid = torch.arange(B, dtype=torch.int32, device="cuda")
+    rows_sid = torch.repeat_interleave(sid, q_len)
+    pos = torch.from_numpy(np.concatenate([np.arange(L - q_len, L) for L in lens]).astype(np.int32)).cuda()
+    junk = torch.from_numpy(rng.standard_normal((B * q_len, Hkv, D)).astype(np.float32) * 5).cuda()
+    rkv.append_q8(ctx, sc.g, fused, sc.bt_d, rows_sid, pos, junk, -junk)
+    kn = np.concatenate([_last_rows(sc, b, q_len)[0] for b in range(B)])
+    vn = np.concatenate([_last_rows(sc, b, q_len)[1] for b in range(B)])
+    kd = torch.from_numpy(kn).cuda().to(torch.bfloat16)
+    vd = torch.from_numpy(vn).cuda().to(torch.bfloat16)
+    q = rng.standard_normal((B, q_len, Hq, D)).astype(np.float32)
+    q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    qd = torch.from_numpy(q).cuda().to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+    outs = []
+    for pages, app in ((sc.pages_d, None), (fused, rkv.append_args(rows_sid, pos, kd, vd, rule=rule))):
+        out = torch.empty((B, q_len, Hq, D), dtype=torch.float32, device="cuda")
+        a = rkv.decode_args(qd, out, sid, scale, max(lens), q_len=q_len, partition_tokens=part)
+        ws = torch.empty(max(rkv.decode_workspace_bytes(sc.g, a), 4), dtype=torch.uint8, device="cuda")
+        a = rkv.decode_args(qd, out, sid, scale, max(lens), q_len=q_len, partition_tokens=part,
+                            workspace=ws, append=app)
+        rkv.decode_q8(ctx, sc.g, pages, sc.bt_d, sc.lens_d, a)
+        ctx.sync()
+        outs.append(out.cpu().numpy())
+    assert torch.equal(fused, sc.pages_d), "pages written by the decode's append differ"
+    assert np.array_equal(outs[0], outs[1])
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(B, dtype=np.int32), q,
+                            scale, part)
+    assert_close(outs[1], want, what="append-in-decode")
+
+
+def test_append_in_decode_bad_rows_are_reported(rkv, rko, ctx):
+    """A row whose sequence is not its batch entry's (fault bit 4) or whose
+    position is at or past the sequence length (fault bit 2) is reported by
+    rkv_ctx_sync and writes nothing."""
+    torch = _torch()
+    Hq, Hkv, D, PT = 8, 2, 128, 32
+    sc = Scene(rkv, rko, Hkv, D, PT, [100, 200], seed=9)
+    sid = torch.arange(2, dtype=torch.int32, device="cuda")
+    q = torch.randn((2, 1, Hq, D), device="cuda")
+    rows = torch.randn((2, Hkv, D), device="cuda")
+    for rows_sid, pos, bit in (([1, 1], [50, 60], 4), ([0, 1], [100, 60], 2)):
+        pages = sc.pages_d.clone()
+        out = torch.empty_like(q)
+        app = rkv.append_args(torch.tensor(rows_sid, dtype=torch.int32, device="cuda"),
+                              torch.tensor(pos, dtype=torch.int32, device="cuda"), rows, rows)
+        a = rkv.decode_args(q, out, sid, 0.1, 200, partition_tokens=64)
+        ws = torch.empty(rkv.decode_workspace_bytes(sc.g, a), dtype=torch.uint8, device="cuda")
+        a = rkv.decode_args(q, out, sid, 0.1, 200, partition_tokens=64, workspace=ws, append=app)
+        rkv.decode_q8(ctx, sc.g, pages, sc.bt_d, sc.lens_d, a)
+        with pytest.raises(rkv.RkvError) as ei:
+            ctx.sync()
+        assert ei.value.status == rkv.ERR_BAD_BLOCK_TABLE and f"0x{bit:x}" in str(ei.value)
+        # only the valid row of the pair was written
+        valid = [i for i in range(2) if not (rows_sid[i] != i or pos[i] >= sc.lens[i])]
+        ref = sc.pages_d.clone()
+        if valid:
+            rkv.append_q8(ctx, sc.g, ref, sc.bt_d, torch.tensor([rows_sid[i] for i in valid], dtype=torch.int32, device="cuda"),
+                          torch.tensor([pos[i] for i in valid], dtype=torch.int32, device="cuda"),
+                          rows[valid], rows[valid])
+        ctx.sync()
+        assert torch.equal(pages, ref)
+
+
 def _as_u8(ptr, n):
     """A uint8 torch view of n bytes of device memory owned by the pool."""
     torch = _torch()
