@@ -57,6 +57,9 @@ def parse():
     ap.add_argument("--head-dim", type=int, default=256)
     ap.add_argument("--page-size", type=int, default=64)
     ap.add_argument("--partition-tokens", type=int, default=0)
+    ap.add_argument("--config", type=int, default=1,
+                    help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs")
+    ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
     ap.add_argument("--append-launch", action="store_true",
                     help="append the step's rows with a separate rkv_pool_append launch instead "
                          "of inside the decode launch")
@@ -131,53 +134,29 @@ def main() -> int:
     q = torch.randn((B, 1, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
     out = torch.empty((B, 1, Hq, D), device=dev, dtype=torch.float32)
     scale = 1.0 / math.sqrt(D)
-    a = rkv.decode_args(q, out, seq_ids, scale, L, partition_tokens=args.partition_tokens)
-    part = rkv.decode_partition_tokens(g, a)
-    n_parts = (L + part - 1) // part
-    rows = Hq
-    # split-K partials, laid out as rkv_decode_q8's workspace
-    ml = torch.empty((B, rows, n_parts, 2), device=dev, dtype=torch.float32)
-    o = torch.empty((B, rows, n_parts, D), device=dev, dtype=torch.float32)
     stream = torch.cuda.current_stream()
-    lib = rkv.lib()
-    pages_p = pool.layer_pages(0)
-    bt_p = pool.block_tables_ptr()
-    lens_p = pool.seq_lens_ptr()
-
     # this step's new K/V rows, appended by the decode launch itself (the
     # default) or by a separate rkv_pool_append launch (--append-launch)
     app = rkv.append_args(seq_ids, positions, k_new, v_new)
     a = rkv.decode_args(q, out, seq_ids, scale, L, partition_tokens=args.partition_tokens,
                         append=None if args.append_launch else app)
+    ws = torch.empty(max(rkv.decode_workspace_bytes(g, a), 4), device=dev, dtype=torch.uint8)
+    a = rkv.decode_args(q, out, seq_ids, scale, L, partition_tokens=args.partition_tokens,
+                        workspace=ws, append=None if args.append_launch else app)
     fused = not args.append_launch
+    rows = Hq
 
     def step(ev=None):
-        # [append launch], then the two kernels rkv_pool_decode chains (split-K
-        # decode, log-sum-exp combine), called through their kernel-level entry
-        # points so events can bracket each kernel on the launch stream
+        # [append launch], then rkv_pool_decode: the split-K decode kernel and
+        # the combine kernel; the library records ev[2] between the two
         if ev is not None:
             ev[0].record(stream)
         if not fused:
             pool.append(0, seq_ids, positions, k_new, v_new, stream=stream)
             if ev is not None:
                 ev[1].record(stream)
-        if n_parts > 1:
-            rkv.check(lib.rkv_decode_q8_partials(ctx.h, C.byref(g), C.c_void_p(pages_p),
-                                                 C.c_void_p(bt_p), pages_per_seq,
-                                                 C.c_void_p(lens_p), B, C.byref(a),
-                                                 C.c_void_p(ml.data_ptr()), C.c_void_p(o.data_ptr()),
-                                                 C.c_void_p(stream.cuda_stream)))
-            if ev is not None:
-                ev[2].record(stream)
-            rkv.check(lib.rkv_splitk_combine(ctx.h, C.c_void_p(ml.data_ptr()),
-                                             C.c_void_p(o.data_ptr()), B, rows, n_parts, D,
-                                             C.c_void_p(seq_ids.data_ptr()), C.c_void_p(lens_p), B,
-                                             part, C.c_void_p(out.data_ptr()), rkv.F32,
-                                             C.c_void_p(stream.cuda_stream)))
-        else:
-            pool.decode(0, a, stream=stream)
-            if ev is not None:
-                ev[2].record(stream)
+        a.split_event = C.c_void_p(ev[2].cuda_event) if ev is not None else None
+        pool.decode(0, a, stream=stream)
         if ev is not None:
             ev[3].record(stream)
 
@@ -185,6 +164,9 @@ def main() -> int:
         step()
     ctx.sync()
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    for e in evs:  # create the events (torch creates them at their first record)
+        for x in e:
+            x.record(stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
@@ -192,6 +174,8 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ctx.sync()
+    part = int(ws[:4].view(torch.int32).item())  # the partition length the device chose
+    n_parts = (L + part - 1) // part
     dec_from = 0 if fused else 1  # the decode launch starts after the append launch
     t_step = [evs[i][0].elapsed_time(evs[i][3]) * 1e-3 for i in range(args.steps)]
     t_app = [0.0 if fused else evs[i][0].elapsed_time(evs[i][1]) * 1e-3 for i in range(args.steps)]
@@ -324,5 +308,338 @@ def cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv, D, scal
             "gpu_vs_cpu_max_abs_err_on_sample": max_err}
 
 
+# ---------------------------------------------------------------------------
+# Secondary workloads: `--config N` prints one
+# JSON line of the same shape for that workload.  The default run above is
+# the headline line the metric is quoted on.
+# ---------------------------------------------------------------------------
+
+def _fill_layer(rkv, pool, layer, seqs, lens, Hkv, D, seed, outlier_frac=0.0, chunk=1 << 16):
+    """Append rows [0, lens[i]) of sequence seqs[i] to `layer`: bf16 N(0,1)
+    K/V (seeded per layer), with ceil(outlier_frac*D) seed-chosen channels
+    per kv head scaled x8 before quantization.  Returns nothing; not timed."""
+    import numpy as np
+    import torch
+    dev = torch.device("cuda:0")
+    sid = np.concatenate([np.full(int(L), s, np.int32) for s, L in zip(seqs, lens)])
+    pos = np.concatenate([np.arange(int(L), dtype=np.int32) for L in lens])
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1000 + 7919 * layer + seed)
+    mult = None
+    if outlier_frac > 0:
+        rng = np.random.default_rng(seed * 131 + layer)
+        m = np.ones((Hkv, D), np.float32)
+        for h in range(Hkv):
+            m[h, rng.choice(D, int(math.ceil(outlier_frac * D)), replace=False)] = 8.0
+        mult = torch.from_numpy(m).to(dev)
+    for a in range(0, len(sid), chunk):
+        n = min(chunk, len(sid) - a)
+        k = torch.randn((n, Hkv, D), generator=gen, device=dev)
+        v = torch.randn((n, Hkv, D), generator=gen, device=dev)
+        if mult is not None:
+            k *= mult
+            v *= mult
+        pool.append(layer, torch.from_numpy(sid[a:a + n]).to(dev), torch.from_numpy(pos[a:a + n]).to(dev),
+                    k.to(torch.bfloat16), v.to(torch.bfloat16))
+
+
+class _Decoder:
+    """One layer-step through rkv_pool_decode (split-K decode with the rows
+    appended inside it, then the combine); the library records the split
+    event of `ev` between the two kernels."""
+
+    def __init__(self, rkv, ctx, pool, q, out, seq_ids, scale, max_len, q_len, app, part, stream):
+        import torch
+        self.rkv, self.pool, self.stream = rkv, pool, stream
+        g = pool.geometry
+        a = rkv.decode_args(q, out, seq_ids, scale, max_len, q_len=q_len, partition_tokens=part,
+                            append=app)
+        self.ws = torch.empty(max(rkv.decode_workspace_bytes(g, a), 4), device="cuda", dtype=torch.uint8)
+        self.a = rkv.decode_args(q, out, seq_ids, scale, max_len, q_len=q_len, partition_tokens=part,
+                                 workspace=self.ws, append=app)
+        self.max_len = max_len
+
+    def __call__(self, layer, ev=None):
+        if ev is not None:
+            ev[0].record(self.stream)
+        self.a.split_event = C.c_void_p(ev[1].cuda_event) if ev is not None else None
+        self.pool.decode(layer, self.a, stream=self.stream)
+
+    def partition_tokens(self) -> int:
+        """The partition length of the last launch (workspace header)."""
+        import torch
+        return int(self.ws[:4].view(torch.int32).item())
+
+
+def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extra):
+    value = step_bytes / step_s / 1e9
+    res = {
+        "metric": f"config {cfg}: paged Q8 decode HBM GB/s (% of 8 TB/s) + us/step",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 QK + f16 PV, f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
+        "config": dict(workload=workload, **extra.pop("config", {})),
+        "us_per_step": round(step_s * 1e6, 2),
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "algorithmic_bytes_per_step": step_bytes,
+        "achieved_tflops": round(flops / step_s / 1e12, 2),
+    }
+    if dec_s:
+        res["roofline"] = {"bound": "hbm", "kernel": "decode_kernel",
+                           "achieved": round(dec_bytes / dec_s / 1e9, 2), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
+                           "traffic": None, "algorithmic_bytes_per_launch": dec_bytes,
+                           "decode_us": round(dec_s * 1e6, 2)}
+    res.update(extra)
+    print(json.dumps(res), flush=True)
+
+
+def _time_steps(args, stream, step, n_events=2):
+    import torch
+    for i in range(args.warmup):
+        step(i, None)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_events)] for _ in range(args.steps)]
+    for e in evs:  # create the events (torch creates them at their first record)
+        for x in e:
+            x.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    dec = sum(e[0].elapsed_time(e[1]) for e in evs) * 1e-3 / args.steps
+    return wall, dec
+
+
+def run_config(args) -> int:
+    """Configs 2, 3 and 5: every sequence keeps its length across steps (the
+    appended rows overwrite the same slots), pools rotate over `layers` so the
+    K/V stream does not fit the 256 MB Infinity Cache.  Config 5 also grows
+    each sequence by its 4 draft rows and rolls back to a seeded accepted
+    length every step, through the allocator and an async table upload."""
+    import numpy as np
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    cfg = args.config
+    rng = np.random.default_rng(args.seed)
+    Hq, Hkv, D, PT = 16, 2, 256, 64
+    q_len, outliers, part = 1, 0.0, args.partition_tokens
+    if cfg == 2:
+        B, layers = 16, 8
+        lens = rng.integers(4096, 16385, B)
+        outliers = 0.01
+        work = (f"config 2 batched decode: B=16, L~U[4096,16384] (sum {int(lens.sum())}), Hq=16, Hkv=2, "
+                f"D=256, page 64, 1% outlier channels x8, {layers} rotating layer pools")
+    elif cfg == 3:
+        B, layers = 1, 2
+        lens = np.array([262144])
+        work = (f"config 3 long context: B=1, L=262144, Hq=16, Hkv=2, D=256, page 64, "
+                f"{'device-chosen' if not part else 262144 // part} split-K partitions + LSE combine, "
+                f"{layers} rotating layer pools")
+    elif cfg == 5:
+        B, layers, q_len = 32, 1, 4
+        lens = np.full(B, 32768)
+        work = ("config 5 speculative verify: B=32, q_len=4 causal draft rows, Hq=16, Hkv=2, D=256, "
+                "page 64, L=32768 committed + 4 drafts, seeded accept length in [0,4] and rollback")
+    else:
+        raise SystemExit(f"unknown config {cfg}")
+    cap = lens + q_len
+    pps = int((cap.max() + PT - 1) // PT)
+    num_pages = int(math.ceil(sum((int(c) + PT - 1) // PT for c in cap) * 1.10))
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, num_pages, B, pps, seed=args.seed)
+    for s in range(B):
+        pool.alloc.reserve(s, int(cap[s]) if cfg != 5 else int(lens[s]))
+    pool.sync_tables()
+    for layer in range(layers):
+        _fill_layer(rkv, pool, layer, range(B), lens if cfg == 5 else cap, Hkv, D, args.seed, outliers)
+    ctx.sync()
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 5)
+    seq_ids = torch.arange(B, device=dev, dtype=torch.int32)
+    rows_sid = torch.repeat_interleave(seq_ids, q_len)
+    first = torch.from_numpy(lens.astype(np.int32) if cfg == 5 else (cap - q_len).astype(np.int32)).to(dev)
+    positions = (first.repeat_interleave(q_len) +
+                 torch.arange(q_len, device=dev, dtype=torch.int32).repeat(B)).to(torch.int32)
+    k_new = torch.randn((B * q_len, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((B * q_len, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((B, q_len, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty((B, q_len, Hq, D), device=dev, dtype=torch.float32)
+    app = rkv.append_args(rows_sid, positions, k_new, v_new)
+    dec = _Decoder(rkv, ctx, pool, q, out, seq_ids, 1.0 / math.sqrt(D), int(cap.max()), q_len, app,
+                   part, stream)
+    acc_rng = np.random.default_rng(args.seed + 17)
+    accepts = []
+
+    def step(i, ev):
+        if cfg == 5:
+            for s in range(B):
+                pool.alloc.reserve(s, int(lens[s]) + q_len)
+            pool.sync_tables(stream)
+        dec(i % layers, ev)
+        if cfg == 5:
+            a = acc_rng.integers(0, q_len + 1, B)
+            accepts.append(a)
+            for s in range(B):
+                pool.alloc.truncate(s, int(lens[s] + a[s]))
+                pool.alloc.truncate(s, int(lens[s]))  # steady state: drafts never commit
+
+    wall, dec_s = _time_steps(args, stream, step)
+    ctx.sync()
+    pt = dec.partition_tokens()
+    n_parts = int(sum((int(c) + pt - 1) // pt for c in cap))  # partitions of the batch
+    row = D // 32 * 34
+    kv = int(cap.sum()) * Hkv * 2 * row
+    qo = B * q_len * Hq * D * (2 + 4)
+    bt = sum((int(c) + PT - 1) // PT for c in cap) * 4
+    apb = B * q_len * Hkv * 2 * (D * 2 + row)
+    step_bytes = kv + qo + bt + apb
+    # causal draft rows: row j attends ctx+j+1 positions
+    flops = 4 * D * Hq * sum(int(c) - q_len + j + 1 for c in cap for j in range(q_len))
+    _line(args, cfg, work, wall, dec_s, step_bytes, step_bytes, flops,
+          {"config": {"batch": B, "q_len": q_len, "layers_rotated": layers,
+                      "partition_tokens": pt, "partitions_total": n_parts,
+                      "pool_pages_per_layer": num_pages},
+           "split_k_partial_bytes": n_parts * q_len * Hq * (D + 2) * 4,
+           **({"mean_accept": float(np.mean(accepts))} if accepts else {})})
+    pool.close()
+    ctx.close()
+    return 0
+
+
+def run_config4(args) -> int:
+    """Continuous-batching mix: B=64 slots with lognormal lengths (median
+    8192, sigma 1.0, clipped to [512, 65536]) over 48 layer pools.  Per step
+    and layer: 56 slots decode one token (appended inside the decode launch)
+    and 8 rotating slots append a 512-row prefill chunk; each slot finishes
+    with probability 0.02 per step, frees its pages and restarts empty.  The
+    allocator edits of a step go up in one async table upload."""
+    import numpy as np
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    rng = np.random.default_rng(args.seed)
+    B, layers, Hq, Hkv, D, PT = 64, args.layers, 16, 2, 256, 64
+    NPF, CH = 8, 512
+    lens = np.clip(np.round(np.exp(rng.normal(math.log(8192), 1.0, B))), 512, 65536).astype(np.int64)
+    total_steps = args.warmup + args.steps
+    # worst case growth: every slot prefills every step
+    max_len = 65536 + total_steps * CH
+    pps = (max_len + PT - 1) // PT
+    num_pages = int(math.ceil((int(lens.sum()) + B * total_steps * CH // 4) / PT * 1.10)) + B * 8
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, num_pages, B, pps, seed=args.seed)
+    for s in range(B):
+        pool.alloc.reserve(s, int(lens[s]))
+    pool.sync_tables()
+    for layer in range(layers):
+        _fill_layer(rkv, pool, layer, range(B), lens, Hkv, D, args.seed)
+    ctx.sync()
+    stream = torch.cuda.current_stream()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 9)
+    ND = B - NPF
+    kd = torch.randn((ND, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    vd = torch.randn((ND, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    kp = torch.randn((NPF * CH, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    vp = torch.randn((NPF * CH, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((ND, 1, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty((ND, 1, Hq, D), device=dev, dtype=torch.float32)
+    d_sid = torch.empty(ND, dtype=torch.int32, device=dev)
+    d_pos = torch.empty(ND, dtype=torch.int32, device=dev)
+    p_sid = torch.empty(NPF * CH, dtype=torch.int32, device=dev)
+    p_pos = torch.empty(NPF * CH, dtype=torch.int32, device=dev)
+    # host staging of the per-step index vectors: two pinned buffers, each
+    # rewritten only after the upload that last read it has run
+    h_idx = [torch.empty(2 * ND + 2 * NPF * CH, dtype=torch.int32).pin_memory() for _ in range(2)]
+    h_done = [None, None]
+    app = rkv.append_args(d_sid, d_pos, kd, vd)
+    scale = 1.0 / math.sqrt(D)
+    fin_rng = np.random.default_rng(args.seed + 3)
+    cur = lens.copy()
+    stats = {"decode_tokens": 0, "prefill_rows": 0, "finished": 0}
+    dec_cache = {}
+    per_step_bytes = []
+
+    def step(i, ev):
+        pf = [(i * NPF + j) % B for j in range(NPF)]
+        dset = [s for s in range(B) if s not in pf]
+        # finishes: free pages, restart empty (new sequences take pages from the free list)
+        for s in range(B):
+            if fin_rng.random() < 0.02:
+                pool.alloc.free(s)
+                cur[s] = 0
+                stats["finished"] += 1
+        dpos = cur[dset].copy()
+        for s in dset:
+            pool.alloc.reserve(s, int(cur[s]) + 1)
+            cur[s] += 1
+        ppos0 = cur[pf].copy()
+        for s in pf:
+            pool.alloc.reserve(s, int(cur[s]) + CH)
+            cur[s] += CH
+        hb = i & 1
+        if h_done[hb] is not None:
+            h_done[hb].synchronize()
+        h = h_idx[hb].numpy()
+        h[:ND] = dset
+        h[ND:2 * ND] = dpos
+        h[2 * ND:2 * ND + NPF * CH] = np.repeat(pf, CH)
+        h[2 * ND + NPF * CH:] = (ppos0[:, None] + np.arange(CH)[None, :]).reshape(-1)
+        dev_idx = h_idx[hb].to(dev, non_blocking=True)
+        h_done[hb] = torch.cuda.Event()
+        h_done[hb].record(stream)
+        d_sid.copy_(dev_idx[:ND])
+        d_pos.copy_(dev_idx[ND:2 * ND])
+        p_sid.copy_(dev_idx[2 * ND:2 * ND + NPF * CH])
+        p_pos.copy_(dev_idx[2 * ND + NPF * CH:])
+        pool.sync_tables(stream)
+        max_len = int(cur[dset].max())
+        key = (max_len + 4095) // 4096
+        if key not in dec_cache:
+            dec_cache[key] = _Decoder(rkv, ctx, pool, q, out, d_sid, scale, key * 4096, 1, app, 0, stream)
+        dec = dec_cache[key]
+        if ev is not None:
+            ev[0].record(stream)
+        for layer in range(layers):
+            pool.append(layer, p_sid, p_pos, kp, vp, stream=stream)
+            dec(layer)
+        if ev is not None:
+            ev[1].record(stream)
+        stats["decode_tokens"] += int(cur[dset].sum())
+        stats["prefill_rows"] += NPF * CH
+        row = D // 32 * 34
+        per_step_bytes.append(layers * (int(cur[dset].sum()) * Hkv * 2 * row + ND * Hq * D * 6 +
+                                        sum((int(cur[s]) + PT - 1) // PT for s in dset) * 4 +
+                                        (ND + NPF * CH) * Hkv * 2 * (D * 2 + row)))
+
+    wall, tot = _time_steps(args, stream, step)
+    ctx.sync()
+    timed = per_step_bytes[args.warmup:]
+    step_bytes = int(sum(timed) / len(timed))
+    _line(args, 4, f"config 4 continuous batching: B=64 (56 decode + 8 x 512-row prefill append per step), "
+                   f"lognormal L (median 8192, sigma 1.0, [512, 65536]), {layers} layer pools, "
+                   f"2% finish per step", wall, None, step_bytes, step_bytes, 0,
+          {"config": {"layers": layers, "pool_pages_per_layer": num_pages},
+           "us_per_layer_step": round(wall * 1e6 / layers, 2),
+           "event_us_per_step": round(tot * 1e6, 2),
+           "finished_total": stats["finished"]})
+    pool.close()
+    ctx.close()
+    return 0
+
+
 if __name__ == "__main__":
+    _a = parse()
+    if _a.config == 4:
+        sys.exit(run_config4(_a))
+    if _a.config in (2, 3, 5):
+        sys.exit(run_config(_a))
     sys.exit(main())

@@ -141,7 +141,11 @@ typedef struct rkv_decode_args {
   void *out;                /* device [B][q_len][q_heads][head_dim] */
   int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
   int32_t partition_tokens; /* split-K partition length: a multiple of max(32,
-                               page_tokens), at most 64*page_tokens; 0 = auto */
+                               page_tokens), at most 64*page_tokens; 0 = chosen
+                               per launch on the device from the batch's
+                               lengths (the smallest such length, >= 256,
+                               whose partitions fill one round of resident
+                               workgroups) */
   int32_t max_seq_len;      /* >= every seq_lens[seq_ids[b]]; sizes the grid */
   void *workspace;          /* device scratch for the split-K partials, of
                                rkv_decode_workspace_bytes (may be NULL when one
@@ -157,6 +161,9 @@ typedef struct rkv_decode_args {
                                one launch fewer per step (the reference step
                                quantizes, then dispatches the decode:
                                har-serve-vulkan-attn-smoke.rs:62-69, 149-161). */
+  void *split_event;        /* optional hipEvent_t, recorded on the stream
+                               between the decode kernel and the combine kernel
+                               (per-kernel timing); NULL = none */
 } rkv_decode_args;
 
 /* ---- kernel-level entry points (explicit device pointers) -----------------
@@ -179,16 +186,20 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
                          const int32_t *block_tables, int32_t bt_stride,
                          const int32_t *seq_lens, int32_t n_seqs,
                          const rkv_decode_args *args, void *stream);
-/* Workspace bytes rkv_decode_q8 needs for these arguments (0 if none). */
+/* Workspace bytes rkv_decode_q8 needs for these arguments (0 if none); it
+ * depends on batch, q_len, q_heads, max_seq_len and partition_tokens, and
+ * needs no initialisation. */
 size_t rkv_decode_workspace_bytes(const rkv_kv_geometry *g, const rkv_decode_args *args);
-/* Partition length rkv_decode_q8 uses for these arguments. */
+/* The explicit partition length of these arguments, or 0 when the device
+ * chooses it per launch. */
 int32_t rkv_decode_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *args);
 
 /* Split-K stage alone (for parity tests): writes per-partition partials
  * (m, l) into ml [B][q_len*q_heads][n_parts][2] and o into
  * o [B][q_len*q_heads][n_parts][head_dim].  m is the running max of
  * scale*log2(e)*q.k (base-2 domain); l and o are unnormalised sums of
- * 2^(s - m) and 2^(s - m) * v.  n_parts = ceil(max_seq_len/partition_tokens). */
+ * 2^(s - m) and 2^(s - m) * v.  n_parts = ceil(max_seq_len/partition_tokens);
+ * partition_tokens must be explicit (> 0). */
 rkv_status rkv_decode_q8_partials(rkv_ctx *ctx, const rkv_kv_geometry *g,
                                   const void *pages, const int32_t *block_tables,
                                   int32_t bt_stride, const int32_t *seq_lens,
@@ -258,6 +269,11 @@ typedef struct rkv_pool rkv_pool;
 rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **out);
 rkv_status rkv_pool_destroy(rkv_pool *pool);
 rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
+/* Upload the allocator's changed block-table rows and all lengths, ordered
+ * on `stream`: launches enqueued on `stream` afterwards see the new tables,
+ * earlier ones the old.  One pinned-staging copy plus one small kernel; the
+ * host waits only if the staging buffer of the call before last is still in
+ * flight.  Use one stream for a pool's syncs and launches. */
 rkv_status rkv_pool_sync_tables(rkv_pool *pool, void *stream);
 /* Device pointers owned by the pool. */
 void *rkv_pool_layer_pages(rkv_pool *pool, int32_t layer);

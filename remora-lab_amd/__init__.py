@@ -63,7 +63,7 @@ class DecodeArgs(C.Structure):
                 ("q_len", C.c_int32), ("q_heads", C.c_int32), ("scale", C.c_float),
                 ("out", P), ("out_dtype", C.c_int32), ("partition_tokens", C.c_int32),
                 ("max_seq_len", C.c_int32), ("workspace", P), ("workspace_bytes", C.c_size_t),
-                ("append", C.POINTER(AppendArgs))]
+                ("append", C.POINTER(AppendArgs)), ("split_event", P)]
 
 
 class FlashDecodeParams(C.Structure):
@@ -290,9 +290,10 @@ def append_args(seq_ids, positions, k_src, v_src, rule=Q8_CANONICAL) -> AppendAr
 
 
 def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0,
-                workspace=None, append: AppendArgs | None = None) -> DecodeArgs:
+                workspace=None, append: AppendArgs | None = None, split_event=None) -> DecodeArgs:
     """`append` (optional): rows [batch*q_len] the decode launch appends
-    before attending over them."""
+    before attending over them.  `split_event` (optional): a hipEvent_t handle
+    (int) recorded between the decode and the combine kernel."""
     import torch
     B = seq_ids.numel()
     q_heads = q.shape[-2]
@@ -301,7 +302,8 @@ def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0
                    BF16 if out.dtype == torch.bfloat16 else F32, partition_tokens,
                    max_seq_len, _ptr(workspace),
                    0 if workspace is None else workspace.numel() * workspace.element_size(),
-                   C.pointer(append) if append is not None else None)
+                   C.pointer(append) if append is not None else None,
+                   P(split_event) if split_event else None)
     a._refs = (q, out, seq_ids, workspace, append)  # the struct holds raw pointers
     return a
 

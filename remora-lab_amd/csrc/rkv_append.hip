@@ -145,6 +145,33 @@ hipError_t launch_import(const Geo &g, uint8_t *pages, const int32_t *bt, int32_
   return hipGetLastError();
 }
 
+namespace {
+// Unpack a block-table update: `n_rows` records of [seq][W page ids] then
+// the lengths of all `n_seqs` sequences.  Block i < n_rows copies record i;
+// block n_rows copies the lengths.
+__global__ __launch_bounds__(256) void table_scatter_kernel(const int32_t *packed, int32_t n_rows,
+                                                           int32_t W, int32_t n_seqs,
+                                                           int32_t *tables, int32_t *lens) {
+  const int32_t r = blockIdx.x;
+  if (r < n_rows) {
+    const int32_t *rec = packed + (int64_t)r * (W + 1);
+    const int32_t seq = rec[0];
+    if (seq < 0 || seq >= n_seqs) return;  // packed by the host from its own table
+    for (int32_t i = threadIdx.x; i < W; i += 256) tables[(int64_t)seq * W + i] = rec[1 + i];
+  } else {
+    const int32_t *src = packed + (int64_t)n_rows * (W + 1);
+    for (int32_t i = threadIdx.x; i < n_seqs; i += 256) lens[i] = src[i];
+  }
+}
+}  // namespace
+
+hipError_t launch_table_scatter(const int32_t *packed, int32_t n_rows, int32_t W, int32_t n_seqs,
+                                int32_t *tables, int32_t *lens, hipStream_t s) {
+  hipLaunchKernelGGL(table_scatter_kernel, dim3((unsigned)n_rows + 1), dim3(256), 0, s, packed,
+                     n_rows, W, n_seqs, tables, lens);
+  return hipGetLastError();
+}
+
 hipError_t launch_f32_to_f16(const float *in, uint16_t *out, int64_t n, int32_t rule,
                              hipStream_t s) {
   if (n == 0) return hipSuccess;

@@ -55,6 +55,117 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineLaunch c) {
   else static_cast<float *>(c.out)[oi] = r;
 }
 
+// Flat-layout combine.  Block (row, entry, split) merges partitions
+// [64*split, 64*split + 64) of the entry (from the header the decode wrote):
+// its 256 threads form groups of head_dim/4 threads (4 dims each, float4
+// loads); group g takes partitions g, g + groups, ... eight at a time with
+// all their loads in flight, merged online (running max, rescaled sums),
+// then the groups merge through LDS.  One split writes the output; with
+// more, every split stores its (m, l, o) and the last to arrive merges them.
+// All merges are the chunk combine of attention.rs:205-212 in base 2.
+struct Merge {
+  float m, l;
+  float4 o;
+  __device__ void add(float mi, float li, float4 oi) {
+    if (mi == -INFINITY) return;
+    const float mn = fmaxf(m, mi);
+    const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+    const float w = __builtin_amdgcn_exp2f(mi - mn);
+    l = l * a + li * w;
+    o.x = o.x * a + oi.x * w;
+    o.y = o.y * a + oi.y * w;
+    o.z = o.z * a + oi.z * w;
+    o.w = o.w * a + oi.w * w;
+    m = mn;
+  }
+};
+
+__global__ __launch_bounds__(256) void combine_flat_kernel(FlatCombineLaunch c) {
+  const int row = blockIdx.x;  // j * q_heads + h
+  const int b = blockIdx.y;
+  const int split = blockIdx.z;
+  const int t = threadIdx.x;
+  const int GS = c.head_dim / 4;  // threads per group
+  const int NG = 256 / GS;        // groups
+  const int grp = t / GS, dt = t % GS;
+  const int rows = c.q_len * c.q_heads;
+  const int j = row / c.q_heads, h = row % c.q_heads;
+  const int q_per_kv = c.q_heads / c.kv_heads;
+  const int kvh = h / q_per_kv;
+  const int R = c.q_len * q_per_kv;
+  const int r = j * q_per_kv + h % q_per_kv;
+  const int32_t start = c.hdr[1 + 2 * b];
+  int32_t n = c.hdr[2 + 2 * b];
+  if (start < 0 || n < 1 || start > c.n_wg - n) n = 0;
+  const int32_t n_splits = n > 0 ? (n + kCombineChunk - 1) / kCombineChunk : 1;
+  if (split >= n_splits) return;
+  const int32_t i_end = min(n, (split + 1) * kCombineChunk);
+  const int64_t p0 = ((int64_t)kvh * c.n_wg + start) * R + r;  // partition i at p0 + i*R
+
+  Merge mg{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
+  for (int32_t i0 = split * kCombineChunk + grp; i0 < i_end; i0 += 8 * NG) {
+    float2 ml[8];
+    float4 ov[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int32_t i = i0 + k * NG;
+      const int64_t pr = p0 + (int64_t)i * R;
+      const bool in = i < i_end;
+      ml[k] = in ? *reinterpret_cast<const float2 *>(c.ml + 2 * pr) : float2{-INFINITY, 0.0f};
+      ov[k] = in ? *reinterpret_cast<const float4 *>(c.o + pr * c.head_dim + 4 * dt)
+                 : float4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) mg.add(ml[k].x, ml[k].y, ov[k]);
+  }
+
+  __shared__ float s_m[8], s_l[8];
+  __shared__ float4 s_o[8][64];
+  if (dt == 0) {
+    s_m[grp] = mg.m;
+    s_l[grp] = mg.l;
+  }
+  s_o[grp][dt] = mg.o;
+  __syncthreads();
+  if (grp != 0) return;
+  Merge tot{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
+  for (int g = 0; g < NG; ++g) tot.add(s_m[g], s_l[g], s_o[g][dt]);
+
+  const int64_t orow = (int64_t)b * rows + row;
+  if (n_splits > 1) {
+    // publish this split; the last split of the row merges all of them
+    float *sm = c.split_ml + 2 * (orow * c.splits + split);
+    if (dt == 0) *reinterpret_cast<float2 *>(sm) = float2{tot.m, tot.l};
+    *reinterpret_cast<float4 *>(c.split_o + (orow * c.splits + split) * c.head_dim + 4 * dt) = tot.o;
+    __threadfence();
+    // group 0 is (part of) wave 0: lane 0's count reaches the group by a shuffle
+    int last = 0;
+    if (dt == 0) last = atomicAdd(c.cnt + orow, 1) == n_splits - 1;
+    last = __shfl(last, 0);
+    if (!last) return;
+    __threadfence();
+    tot = Merge{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
+    for (int32_t q = 0; q < n_splits; ++q) {
+      const float2 v = *reinterpret_cast<const float2 *>(c.split_ml + 2 * (orow * c.splits + q));
+      const float4 o =
+          *reinterpret_cast<const float4 *>(c.split_o + (orow * c.splits + q) * c.head_dim + 4 * dt);
+      tot.add(v.x, v.y, o);
+    }
+  }
+  const float inv = tot.l > 0.0f ? 1.0f / tot.l : 0.0f;
+  const float4 res = tot.l > 0.0f ? float4{tot.o.x * inv, tot.o.y * inv, tot.o.z * inv, tot.o.w * inv}
+                                  : float4{0.f, 0.f, 0.f, 0.f};
+  const int64_t oi = orow * c.head_dim + 4 * dt;
+  if (c.out_bf16) {
+    uint16_t *dst = static_cast<uint16_t *>(c.out) + oi;
+    const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(res.x) | ((uint32_t)f32_to_bf16_rtne(res.y) << 16);
+    const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(res.z) | ((uint32_t)f32_to_bf16_rtne(res.w) << 16);
+    *reinterpret_cast<uint2 *>(dst) = uint2{w0, w1};
+  } else {
+    *reinterpret_cast<float4 *>(static_cast<float *>(c.out) + oi) = res;
+  }
+}
+
 template <int D, int NS>
 hipError_t launch_decode_d(const DecodeLaunch &d, int NT, hipStream_t s) {
   if (NT == 1) return launch_decode_t<D, 1, NS>(d, s);
@@ -64,7 +175,7 @@ hipError_t launch_decode_d(const DecodeLaunch &d, int NT, hipStream_t s) {
 }  // namespace
 
 hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s) {
-  if (d.batch == 0 || d.n_parts == 0) return hipSuccess;
+  if (d.batch == 0 || d.n_wg == 0) return hipSuccess;
   const int R = d.q_len * (d.q_heads / d.g.kv_heads);
   const int NT = R <= 8 ? 1 : (R <= 16 ? 2 : 4);
   if (NT == 4) return launch_decode_rows32(d, s);
@@ -72,6 +183,14 @@ hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s) {
   if (d.g.head_dim == 256)
     return three ? launch_decode_d<256, 3>(d, NT, s) : launch_decode_d<256, 2>(d, NT, s);
   return three ? launch_decode_d<128, 3>(d, NT, s) : launch_decode_d<128, 2>(d, NT, s);
+}
+
+hipError_t launch_combine_flat(const FlatCombineLaunch &c, hipStream_t s) {
+  if (c.batch == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_flat_kernel,
+                     dim3((unsigned)(c.q_len * c.q_heads), (unsigned)c.batch, (unsigned)c.splits),
+                     dim3(256), 0, s, c);
+  return hipGetLastError();
 }
 
 hipError_t launch_combine(const CombineLaunch &c, hipStream_t s) {

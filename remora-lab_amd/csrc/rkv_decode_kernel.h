@@ -208,7 +208,7 @@ struct Decoder {
 
   const DecodeLaunch &p;
   int lane, li, lg, kvh, b;
-  int32_t seq, len, tok0, n_tiles;
+  int32_t seq, len, tok0, tok_end, n_tiles;
   int32_t app_mode;        // 0: no rows to append here; 1: before the first copy; 2: after the prologue copies
   int32_t pg_first;        // first page index (within the sequence) of the partition
   int32_t pidv;            // lane i: page id of the partition's i-th page
@@ -266,7 +266,7 @@ struct Decoder {
     for (int j = 0; j < p.q_len; ++j) {
       const int32_t row = b * p.q_len + j;
       const int32_t pos = p.app_pos[row];
-      if (p.app_seq_ids[row] != seq || pos < tok0 || pos >= tok0 + p.part_tokens || pos >= len) continue;
+      if (p.app_seq_ids[row] != seq || pos < tok0 || pos >= tok_end) continue;
       const int32_t page = p.bt[(int64_t)seq * p.bt_stride + pos / g.page_tokens];
       if (page < 0 || page >= g.num_pages) continue;  // reported by the page-id prefetch
       const int32_t slot = pos % g.page_tokens;
@@ -480,6 +480,97 @@ struct Decoder {
 };
 #endif  // __HIP_DEVICE_COMPILE__
 
+// Length of batch entry e, 0 when its sequence id or length is out of range
+// (the entry then has one partition, whose workgroup reports the fault).
+__device__ __forceinline__ int32_t entry_len(const DecodeLaunch &p, int32_t e) {
+  const int32_t sq = p.seq_ids[e];
+  if (sq < 0 || sq >= p.n_seqs) return 0;
+  const int32_t L = p.seq_lens[sq];
+  return (L < 0 || L > p.max_len) ? 0 : L;
+}
+
+// Inclusive prefix sum over the wave: DPP row shifts inside each 16-lane row,
+// then the row totals by readlane (no LDS round trips).
+__device__ __forceinline__ int32_t wave_iscan(int32_t v, int lane) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  const int32_t r0 = __builtin_amdgcn_readlane(v, 15);
+  const int32_t r1 = __builtin_amdgcn_readlane(v, 31);
+  const int32_t r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row >= 1 ? r0 : 0) + (row >= 2 ? r1 : 0) + (row >= 3 ? r2 : 0);
+}
+__device__ __forceinline__ int32_t wave_isum(int32_t v, int lane) {
+  return __builtin_amdgcn_readlane(wave_iscan(v, lane), 63);
+}
+
+// The partition length of the launch and this workgroup's (entry b,
+// partition part of nb).  Every workgroup computes the same length and the
+// same ordering (entries in batch order, partitions in token order), so
+// workgroup x takes the x-th partition.  Returns false past the last one.
+__device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t x, int32_t &pt,
+                                       int32_t &b, int32_t &part, int32_t &nb) {
+  constexpr int kCached = 4;  // lengths of entries < 256 stay in registers
+  int32_t lc[kCached];
+#pragma unroll
+  for (int c = 0; c < kCached; ++c) {
+    const int32_t e = 64 * c + lane;
+    lc[c] = e < p.batch ? entry_len(p, e) : -1;
+  }
+  auto len_at = [&](int c) -> int32_t {
+    if (c < kCached) {
+      int32_t v = lc[0];
+#pragma unroll
+      for (int k = 1; k < kCached; ++k)
+        if (c == k) v = lc[k];
+      return v;
+    }
+    const int32_t e = 64 * c + lane;
+    return e < p.batch ? entry_len(p, e) : -1;
+  };
+  const int n_chunks = (p.batch + 63) / 64;
+  pt = p.part_tokens;
+  if (pt == 0) {
+    auto count = [&](int32_t t) -> int32_t {
+      int32_t tot = 0;
+      for (int c = 0; c < n_chunks; ++c) {
+        const int32_t L = len_at(c);
+        tot += wave_isum(L < 0 ? 0 : (L > 0 ? (L + t - 1) / t : 1), lane);
+      }
+      return tot;
+    };
+    int32_t lo = p.pt_kmin, hi = p.pt_kmax;
+    if (count(hi * p.pt_unit) > p.target_parts) {
+      lo = hi;
+    } else {
+      while (lo < hi) {
+        const int32_t mid = (lo + hi) >> 1;
+        if (count(mid * p.pt_unit) <= p.target_parts) hi = mid;
+        else lo = mid + 1;
+      }
+    }
+    pt = lo * p.pt_unit;
+  }
+  int32_t base = 0;
+  for (int c = 0; c < n_chunks; ++c) {
+    const int32_t L = len_at(c);
+    const int32_t n = L < 0 ? 0 : (L > 0 ? (L + pt - 1) / pt : 1);
+    const int32_t cum = wave_iscan(n, lane);
+    const uint64_t hit = __ballot(L >= 0 && base + cum > x);
+    if (hit != 0) {
+      const int l = __builtin_ctzll(hit);
+      b = 64 * c + l;
+      nb = __builtin_amdgcn_readlane(n, l);
+      part = x - (base + __builtin_amdgcn_readlane(cum, l) - nb);
+      return true;
+    }
+    base += __builtin_amdgcn_readlane(cum, 63);
+  }
+  return false;
+}
+
 template <int D, int NT, bool kSmall, int NS>
 __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -494,11 +585,25 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   dc.li = dc.lane & 15;  // MFMA row/column within a 16-lane group
   dc.lg = dc.lane >> 4;  // MFMA k-group
   const int lane = dc.lane, li = dc.li, lg = dc.lg;
-  const int part = blockIdx.x;
-  const int b = blockIdx.y;
-  const int kvh = blockIdx.z;
+  const int kvh = blockIdx.y;
   dc.kvh = kvh;
   const Geo g = p.g;
+
+  int32_t pt, b, part, nb;
+  if (!locate(p, lane, (int32_t)blockIdx.x, pt, b, part, nb)) return;
+  // the combine finds entry b's partials through the header, written before
+  // any check can end this workgroup
+  if (p.ws_hdr != nullptr && kvh == 0 && lane == 0) {
+    if (blockIdx.x == 0) p.ws_hdr[0] = pt;
+    if (part == 0) {
+      p.ws_hdr[1 + 2 * b] = (int32_t)blockIdx.x;
+      p.ws_hdr[2 + 2 * b] = nb;
+    }
+  }
+  if (p.ws_cnt != nullptr && kvh == 0 && part == 0) {
+    const int32_t rows = p.q_len * p.q_heads;
+    for (int32_t r = lane; r < rows; r += 64) p.ws_cnt[(int64_t)b * rows + r] = 0;
+  }
 
   const int32_t seq = p.seq_ids[b];
   if (seq < 0 || seq >= p.n_seqs) {
@@ -506,17 +611,17 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
     return;
   }
   const int32_t len = p.seq_lens[seq];
-  if (len < 0 || len > p.bt_stride * g.page_tokens || len > p.n_parts * p.part_tokens) {
+  if (len < 0 || len > p.bt_stride * g.page_tokens || len > p.max_len) {
     if (lane == 0) atomicOr(p.fault, FAULT_BAD_POSITION);
     return;
   }
-  const int32_t tok0 = part * p.part_tokens;
-  if (tok0 >= len && part > 0) return;  // past the end: the combine never reads it
-  const int32_t tok_end = min(len, tok0 + p.part_tokens);
+  const int32_t tok0 = part * pt;
+  const int32_t tok_end = min(len, tok0 + pt);
   dc.b = b;
   dc.seq = seq;
   dc.len = len;
   dc.tok0 = tok0;
+  dc.tok_end = tok_end;
   dc.n_tiles = tok_end > tok0 ? (tok_end - tok0 + kTile - 1) / kTile : 0;
 
   // ---- rows appended by this launch: checked once per batch entry; written
@@ -678,7 +783,9 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
         }
       }
     } else {
-      const int64_t prow = orow * p.n_parts + part;
+      const int64_t prow = p.ws_hdr != nullptr
+                               ? ((int64_t)kvh * p.n_wg + (int64_t)blockIdx.x) * R + row
+                               : orow * p.n_parts + part;
 #pragma unroll
       for (int m = 0; m < D / 16; ++m)
         *reinterpret_cast<v4f *>(p.ws_o + prow * D + 16 * m + 4 * lg) = dc.oacc[np][m];
@@ -691,7 +798,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
 
 template <int D, int NT, int NS>
 hipError_t launch_decode_t(const DecodeLaunch &d, hipStream_t s) {
-  dim3 grid((unsigned)d.n_parts, (unsigned)d.batch, (unsigned)d.g.kv_heads);
+  dim3 grid((unsigned)d.n_wg, (unsigned)d.g.kv_heads);
   if (d.g.page_tokens < kTile)
     hipLaunchKernelGGL((decode_kernel<D, NT, true, NS>), grid, dim3(64), 0, s, d);
   else

@@ -33,6 +33,9 @@ hipError_t launch_import(const Geo &g, uint8_t *pages, const int32_t *bt, int32_
                          int32_t kind, const uint8_t *rows, int32_t *fault, hipStream_t s);
 hipError_t launch_f32_to_f16(const float *in, uint16_t *out, int64_t n, int32_t rule,
                              hipStream_t s);
+// block-table update: records [seq][W ids] x n_rows, then n_seqs lengths
+hipError_t launch_table_scatter(const int32_t *packed, int32_t n_rows, int32_t W, int32_t n_seqs,
+                                int32_t *tables, int32_t *lens, hipStream_t s);
 
 struct DecodeLaunch {
   Geo g;
@@ -48,14 +51,26 @@ struct DecodeLaunch {
   int32_t q_len;
   int32_t q_heads;
   float scale_log2;  // softmax scale * log2(e)
+  // Partition plan.  part_tokens > 0 fixes the partition length; 0 lets every
+  // workgroup derive the same length from the device lengths: the smallest
+  // k*pt_unit, k in [pt_kmin, pt_kmax], whose partition count over the batch
+  // is <= target_parts (else pt_kmax*pt_unit).  Workgroup x of the grid
+  // (n_wg, kv_heads) takes the x-th partition of the batch in entry order.
   int32_t part_tokens;
-  int32_t n_parts;
+  int32_t pt_unit, pt_kmin, pt_kmax, target_parts;
+  int32_t max_len;  // >= every length of the batch
+  int32_t n_wg;     // upper bound of the batch's partition count
+  int32_t n_parts;  // per-entry layout only: ceil(max_len / part_tokens)
   // direct output (ws_o == nullptr) ...
   void *out;
   int32_t out_bf16;
-  // ... or split-K partials [batch][q_len*q_heads][n_parts][2 | head_dim]
+  // ... or split-K partials (m, l) and o, either flat [kv_head][n_wg][R][2 | D]
+  // with ws_hdr = {partition length, then per entry: first partition, count},
+  // or per entry [batch][q_len*q_heads][n_parts][2 | D] (ws_hdr == nullptr)
   float *ws_ml;
   float *ws_o;
+  int32_t *ws_hdr;
+  int32_t *ws_cnt;  // flat layout: [batch][q_len*q_heads] combine counters, zeroed here
   int32_t *fault;
   int32_t stages;  // LDS ring depth: 2 or 3 (tiles in flight = stages - 1)
   // Optional append (app_k == nullptr: none): row b*q_len + j of app_k/app_v
@@ -104,5 +119,29 @@ struct CombineLaunch {
   int32_t out_bf16;
 };
 hipError_t launch_combine(const CombineLaunch &c, hipStream_t s);
+
+// Combine of the flat partials layout written by a decode launch.
+// Blocks (row, entry, split): split s merges partitions [64s, 64s + 64) of
+// the entry; with more than one split the last one to finish merges the
+// splits' results (kept in split_ml / split_o, counted in cnt).
+struct FlatCombineLaunch {
+  const float *ml;
+  const float *o;
+  const int32_t *hdr;
+  int32_t batch;
+  int32_t q_len;
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t n_wg;
+  int32_t splits;    // grid.z: upper bound of ceil(partitions of an entry / 64)
+  float *split_ml;   // [batch][rows][splits][2]
+  float *split_o;    // [batch][rows][splits][head_dim]
+  int32_t *cnt;      // [batch][rows]
+  void *out;
+  int32_t out_bf16;
+};
+constexpr int kCombineChunk = 64;
+hipError_t launch_combine_flat(const FlatCombineLaunch &c, hipStream_t s);
 
 }  // namespace rkv

@@ -173,7 +173,7 @@ struct rkv_alloc {
   std::vector<int32_t> tables;     // [max_seqs][max_pages_per_seq], -1 = none
   std::vector<int32_t> lens;       // [max_seqs]
   std::vector<int32_t> held;       // pages held per sequence
-  std::vector<uint8_t> dirty;      // table row or length changed since last upload
+  std::vector<uint8_t> dirty;      // table row changed since the last upload (lengths always go)
 };
 
 namespace {
@@ -245,9 +245,9 @@ rkv_status rkv_seq_reserve(rkv_alloc *a, int32_t seq, int32_t new_len) {
     row[i] = a->free_list.back();
     a->free_list.pop_back();
   }
+  if (need > a->held[seq]) a->dirty[seq] = 1;
   a->held[seq] = std::max(a->held[seq], need);
   a->lens[seq] = new_len;
-  a->dirty[seq] = 1;
   return RKV_OK;
 }
 
@@ -264,9 +264,9 @@ rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len) {
     a->free_list.push_back(row[i]);
     row[i] = -1;
   }
+  if (keep < a->held[seq]) a->dirty[seq] = 1;
   a->held[seq] = std::min(a->held[seq], keep);
   a->lens[seq] = new_len;
-  a->dirty[seq] = 1;
   return RKV_OK;
 }
 
@@ -315,26 +315,6 @@ rkv_status rkv_alloc_export(const rkv_alloc *a, int32_t *tables, int32_t *lens) 
 namespace {
 
 int32_t decode_stages();
-
-int32_t auto_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *a) {
-  // One full round of resident workgroups: split each sequence into as many
-  // partitions as fit beside the other (batch entry, kv head) pairs, so no
-  // CU waits on a second, partial round.  Partitions are whole pages and
-  // 32-token tiles, at least 256 tokens, at most 64 pages (the kernel keeps
-  // one page id per lane).
-  const int64_t max_len = std::max<int64_t>(a->max_seq_len, 1);
-  const int64_t pairs = std::max<int64_t>((int64_t)a->batch * g->kv_heads, 1);
-  const int32_t rows = a->q_len * (a->q_heads / std::max(g->kv_heads, 1));
-  const int64_t slots = (int64_t)rkv::kComputeUnits *
-                        rkv::decode_wgs_per_cu(g->head_dim, rows, decode_stages());
-  const int64_t parts = std::max<int64_t>(1, slots / pairs);
-  int64_t pt = (max_len + parts - 1) / parts;
-  const int64_t unit = std::max<int32_t>(32, g->page_tokens);
-  pt = std::max<int64_t>(pt, 256);
-  pt = (pt + unit - 1) / unit * unit;
-  pt = std::min<int64_t>(pt, 64 * (int64_t)g->page_tokens);
-  return (int32_t)pt;
-}
 
 rkv_status check_decode(const rkv_kv_geometry *g, const rkv_decode_args *a, const char *op) {
   if (rkv_status s = check_geometry(g, op)) return s;
@@ -391,22 +371,86 @@ int32_t decode_stages() {
   return v;
 }
 
-int32_t parts_of(const rkv_decode_args *a, int32_t pt) {
-  return std::max<int32_t>(1, (a->max_seq_len + pt - 1) / pt);
+// Partition plan of a decode launch (rkv::DecodeLaunch fields).  Explicit
+// partition_tokens fix the length; 0 leaves it to the kernel, which picks the
+// smallest multiple of max(32, page_tokens), at least 256 tokens and at most
+// 64 pages, whose partition count over the batch's actual lengths fills one
+// round of resident workgroups (target = resident slots / kv_heads).
+struct Plan {
+  int32_t pt = 0;  // explicit length, 0 = chosen on the device
+  int32_t unit = 0, kmin = 0, kmax = 0, target = 0;
+  int32_t max_len = 0;
+  int32_t n_wg = 0;     // grid.x: upper bound of the batch's partition count
+  int32_t n_parts = 0;  // explicit: ceil(max_len / pt)
+  bool direct = false;  // one partition covers every sequence: no partials
+};
+
+Plan plan_of(const rkv_kv_geometry *g, const rkv_decode_args *a) {
+  Plan pl;
+  pl.unit = std::max<int32_t>(32, g->page_tokens);
+  pl.kmin = (256 + pl.unit - 1) / pl.unit;
+  pl.kmax = 64 * g->page_tokens / pl.unit;
+  pl.max_len = std::max<int32_t>(a->max_seq_len, 1);
+  const int32_t rows = a->q_len * (a->q_heads / std::max(g->kv_heads, 1));
+  const int64_t slots = (int64_t)rkv::kComputeUnits *
+                        rkv::decode_wgs_per_cu(g->head_dim, rows, decode_stages());
+  pl.target = (int32_t)std::max<int64_t>(1, slots / g->kv_heads);
+  const int64_t B = std::max<int32_t>(a->batch, 0);
+  if (a->partition_tokens > 0) {
+    pl.pt = a->partition_tokens;
+    pl.n_parts = (pl.max_len + pl.pt - 1) / pl.pt;
+    pl.n_wg = (int32_t)std::min<int64_t>(B * pl.n_parts, INT32_MAX);
+    pl.direct = pl.n_parts == 1;
+  } else {
+    const int64_t pmax = (int64_t)pl.kmax * pl.unit;
+    pl.n_wg = (int32_t)std::min<int64_t>(
+        std::max<int64_t>(pl.target, B * ((pl.max_len + pmax - 1) / pmax)), INT32_MAX);
+    pl.direct = pl.max_len <= pl.kmin * pl.unit;
+  }
+  return pl;
 }
 
-// Workspace of a multi-partition decode: partials (m, l) and o of every
-// (row, partition).
-size_t ws_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a, int32_t pt) {
-  const int32_t np = parts_of(a, pt);
-  if (np == 1) return 0;
-  const size_t rows = (size_t)a->batch * a->q_len * a->q_heads * np;
-  return rows * (2 + (size_t)g->head_dim) * sizeof(float);
+int32_t batch_rows_per_kv(const rkv_kv_geometry *g, const rkv_decode_args *a) {
+  return a->q_len * (a->q_heads / g->kv_heads);
+}
+
+// Flat workspace of rkv_decode_q8, each part 256-byte aligned:
+//   header   int32 [1 + 2*batch]: partition length; first partition and
+//            partition count of every entry (written by the decode)
+//   counters int32 [batch][q_len*q_heads] of the combine's splits (zeroed by
+//            the decode)
+//   partials f32 (m, l) then o of every (kv head, partition, row)
+//   splits   f32 (m, l) then o of every (entry, row, combine split)
+// so the workspace needs no initialisation.
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+struct WsLayout {
+  size_t hdr = 0, cnt = 0, ml = 0, o = 0, sml = 0, so = 0, total = 0;
+  int32_t splits = 1;
+};
+WsLayout ws_layout(const rkv_kv_geometry *g, const rkv_decode_args *a, const Plan &pl) {
+  WsLayout w;
+  const size_t B = (size_t)std::max<int32_t>(a->batch, 0);
+  const size_t out_rows = B * a->q_len * a->q_heads;
+  const size_t prows = (size_t)g->kv_heads * pl.n_wg * batch_rows_per_kv(g, a);
+  // an entry has at most min(n_wg, ceil(max_len / shortest partition)) partitions
+  const int64_t shortest = pl.pt > 0 ? pl.pt : (int64_t)pl.kmin * pl.unit;
+  const int64_t n_entry = std::min<int64_t>(pl.n_wg, (pl.max_len + shortest - 1) / shortest);
+  w.splits = (int32_t)std::max<int64_t>(1, (n_entry + rkv::kCombineChunk - 1) / rkv::kCombineChunk);
+  w.cnt = align256(sizeof(int32_t) * (1 + 2 * B));
+  w.ml = w.cnt + align256(sizeof(int32_t) * out_rows);
+  w.o = w.ml + align256(sizeof(float) * 2 * prows);
+  w.sml = w.o + align256(sizeof(float) * prows * g->head_dim);
+  w.so = w.sml + align256(sizeof(float) * 2 * out_rows * w.splits);
+  w.total = w.so + sizeof(float) * out_rows * w.splits * g->head_dim;
+  return w;
+}
+size_t ws_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a, const Plan &pl) {
+  return pl.direct ? 0 : ws_layout(g, a, pl).total;
 }
 
 rkv::DecodeLaunch make_decode(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                               const int32_t *bt, int32_t bt_stride, const int32_t *seq_lens,
-                              int32_t n_seqs, const rkv_decode_args *a, int32_t pt) {
+                              int32_t n_seqs, const rkv_decode_args *a, const Plan &pl) {
   rkv::DecodeLaunch d{};
   d.g = to_geo(g);
   d.pages = static_cast<const uint8_t *>(pages);
@@ -421,8 +465,14 @@ rkv::DecodeLaunch make_decode(rkv_ctx *ctx, const rkv_kv_geometry *g, const void
   d.q_len = a->q_len;
   d.q_heads = a->q_heads;
   d.scale_log2 = a->scale * 1.4426950408889634f;
-  d.part_tokens = pt;
-  d.n_parts = parts_of(a, pt);
+  d.part_tokens = pl.pt;
+  d.pt_unit = pl.unit;
+  d.pt_kmin = pl.kmin;
+  d.pt_kmax = pl.kmax;
+  d.target_parts = pl.target;
+  d.max_len = pl.max_len;
+  d.n_wg = pl.n_wg;
+  d.n_parts = pl.n_parts;
   d.out = a->out;
   d.out_bf16 = a->out_dtype == RKV_BF16;
   d.fault = ctx->d_fault;
@@ -487,12 +537,13 @@ rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
 
 int32_t rkv_decode_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_args *a) {
   if (!g || !a) return 0;
-  return a->partition_tokens > 0 ? a->partition_tokens : auto_partition_tokens(g, a);
+  return a->partition_tokens > 0 ? a->partition_tokens : 0;
 }
 
 size_t rkv_decode_workspace_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a) {
   if (!g || !a || check_geometry(g, "rkv_decode_workspace_bytes") != RKV_OK) return 0;
-  return ws_bytes(g, a, rkv_decode_partition_tokens(g, a));
+  if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0 || a->q_len < 1) return 0;
+  return ws_bytes(g, a, plan_of(g, a));
 }
 
 rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
@@ -505,35 +556,33 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
   if (rkv_status s = check_tables(pages, block_tables, bt_stride, n_seqs, op)) return s;
   if (!seq_lens) return fail(RKV_ERR_INVALID_ARG, op, "seq_lens is NULL");
   if (a->batch == 0) return RKV_OK;
-  const int32_t pt = rkv_decode_partition_tokens(g, a);
-  rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pt);
-  const size_t need = ws_bytes(g, a, pt);
-  if (d.n_parts > 1) {
+  const Plan pl = plan_of(g, a);
+  rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pl);
+  hipStream_t hs = as_stream(stream);
+  if (!pl.direct) {
+    const size_t need = ws_bytes(g, a, pl);
     if (!a->workspace || a->workspace_bytes < need)
-      return fail(RKV_ERR_INVALID_ARG, op, "workspace %zu bytes < %zu needed for %d partitions",
-                  a->workspace_bytes, need, d.n_parts);
-    const size_t rows = (size_t)a->batch * a->q_len * a->q_heads * d.n_parts;
-    d.ws_ml = static_cast<float *>(a->workspace);
-    d.ws_o = d.ws_ml + 2 * rows;
+      return fail(RKV_ERR_INVALID_ARG, op, "workspace %zu bytes < %zu needed", a->workspace_bytes,
+                  need);
+    const WsLayout w = ws_layout(g, a, pl);
+    uint8_t *base = static_cast<uint8_t *>(a->workspace);
+    d.ws_hdr = reinterpret_cast<int32_t *>(base + w.hdr);
+    d.ws_cnt = reinterpret_cast<int32_t *>(base + w.cnt);
+    d.ws_ml = reinterpret_cast<float *>(base + w.ml);
+    d.ws_o = reinterpret_cast<float *>(base + w.o);
   }
-  hipError_t e = rkv::launch_decode(d, as_stream(stream));
+  hipError_t e = rkv::launch_decode(d, hs);
   if (e != hipSuccess) return hip_fail(op, e);
-  if (d.n_parts > 1) {
-    rkv::CombineLaunch c{};
-    c.ml = d.ws_ml;
-    c.o = d.ws_o;
-    c.batch = a->batch;
-    c.rows = a->q_len * a->q_heads;
-    c.n_parts = d.n_parts;
-    c.head_dim = g->head_dim;
-    c.seq_ids = a->seq_ids;
-    c.seq_lens = seq_lens;
-    c.n_seqs = n_seqs;
-    c.part_tokens = pt;
-    c.out = a->out;
-    c.out_bf16 = d.out_bf16;
-    e = rkv::launch_combine(c, as_stream(stream));
-    if (e != hipSuccess) return hip_fail(op, e);
+  if (!pl.direct) {
+    if (a->split_event && (e = hipEventRecord(static_cast<hipEvent_t>(a->split_event), hs)) != hipSuccess)
+      return hip_fail(op, e);
+    const WsLayout w = ws_layout(g, a, pl);
+    uint8_t *base = static_cast<uint8_t *>(a->workspace);
+    rkv::FlatCombineLaunch c{d.ws_ml, d.ws_o, d.ws_hdr, a->batch, a->q_len, a->q_heads,
+                             g->kv_heads, g->head_dim, pl.n_wg, w.splits,
+                             reinterpret_cast<float *>(base + w.sml),
+                             reinterpret_cast<float *>(base + w.so), d.ws_cnt, a->out, d.out_bf16};
+    if ((e = rkv::launch_combine_flat(c, hs)) != hipSuccess) return hip_fail(op, e);
   }
   return RKV_OK;
 }
@@ -547,10 +596,13 @@ rkv_status rkv_decode_q8_partials(rkv_ctx *ctx, const rkv_kv_geometry *g, const 
   if (rkv_status s = check_decode(g, a, op)) return s;
   if (rkv_status s = check_tables(pages, block_tables, bt_stride, n_seqs, op)) return s;
   if (!seq_lens || !ml || !o) return fail(RKV_ERR_INVALID_ARG, op, "NULL seq_lens/ml/o");
+  if (a->partition_tokens <= 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "needs an explicit partition_tokens (the [B][rows][n_parts] "
+                                         "layout is sized by it)");
   if (a->batch == 0) return RKV_OK;
-  const int32_t pt = rkv_decode_partition_tokens(g, a);
-  rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pt);
-  d.ws_ml = ml;  // non-null workspace: the kernel writes partials, even for one partition
+  const Plan pl = plan_of(g, a);
+  rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pl);
+  d.ws_ml = ml;  // per-entry layout, written even for one partition
   d.ws_o = o;
   d.out = nullptr;
   hipError_t e = rkv::launch_decode(d, as_stream(stream));
@@ -736,6 +788,13 @@ struct rkv_pool {
   size_t layer_bytes = 0;
   int32_t *d_tables = nullptr;
   int32_t *d_lens = nullptr;
+  // table uploads: two pinned host staging buffers (reused every other
+  // sync, after the event of their last copy) and one device buffer, all of
+  // the packed size max_seqs * (W + 1) + max_seqs int32
+  int32_t *h_stage[2] = {nullptr, nullptr};
+  hipEvent_t stage_done[2] = {nullptr, nullptr};
+  int32_t *d_stage = nullptr;
+  uint32_t n_syncs = 0;
 };
 
 extern "C" {
@@ -761,10 +820,17 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
   p->layer_bytes = (size_t)desc->num_pages * rkv::page_bytes(to_geo(&g));
   hipError_t e;
   const size_t tbytes = sizeof(int32_t) * (size_t)desc->max_seqs * desc->max_pages_per_seq;
+  const size_t sbytes =
+      sizeof(int32_t) * ((size_t)desc->max_seqs * (desc->max_pages_per_seq + 1) + desc->max_seqs);
   if ((e = hipMalloc(&p->pages, p->layer_bytes * desc->layers)) != hipSuccess ||
       (e = hipMalloc(&p->d_tables, tbytes)) != hipSuccess ||
-      (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess) {
-    rkv_status s = fail(RKV_ERR_DEVICE, op, "hipMalloc of %zu page bytes: %s",
+      (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess ||
+      (e = hipMalloc(&p->d_stage, sbytes)) != hipSuccess ||
+      (e = hipHostMalloc(&p->h_stage[0], sbytes, hipHostMallocDefault)) != hipSuccess ||
+      (e = hipHostMalloc(&p->h_stage[1], sbytes, hipHostMallocDefault)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&p->stage_done[0], hipEventDisableTiming)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&p->stage_done[1], hipEventDisableTiming)) != hipSuccess) {
+    rkv_status s = fail(RKV_ERR_DEVICE, op, "allocating %zu page bytes and tables: %s",
                         p->layer_bytes * desc->layers, hipGetErrorString(e));
     rkv_pool_destroy(p);
     return s;
@@ -778,6 +844,10 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
     rkv_pool_destroy(p);
     return s;
   }
+  if ((e = hipStreamSynchronize(nullptr)) != hipSuccess) {
+    rkv_pool_destroy(p);
+    return hip_fail(op, e);
+  }
   *out = p;
   return RKV_OK;
 }
@@ -785,9 +855,17 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
 rkv_status rkv_pool_destroy(rkv_pool *p) {
   if (!p) return RKV_OK;
   if (p->ctx) (void)hipSetDevice(p->ctx->device);
+  for (int i = 0; i < 2; ++i) {
+    if (p->stage_done[i]) (void)hipEventSynchronize(p->stage_done[i]);
+  }
   (void)hipFree(p->pages);
   (void)hipFree(p->d_tables);
   (void)hipFree(p->d_lens);
+  (void)hipFree(p->d_stage);
+  for (int i = 0; i < 2; ++i) {
+    if (p->h_stage[i]) (void)hipHostFree(p->h_stage[i]);
+    if (p->stage_done[i]) (void)hipEventDestroy(p->stage_done[i]);
+  }
   rkv_alloc_destroy(p->alloc);
   delete p;
   return RKV_OK;
@@ -799,24 +877,36 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   const char *op = "rkv_pool_sync_tables";
   if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
   if (rkv_status s = use_device(p->ctx, op)) return s;
-  // Blocking copies of the changed rows: host-side allocator edits happen
-  // between steps, and the copies are ordered after `stream`'s prior work.
-  hipError_t e = hipStreamSynchronize(as_stream(stream));
-  if (e != hipSuccess) return hip_fail(op, e);
+  // Stream-ordered upload: the changed rows and every length are packed into
+  // a pinned staging buffer, copied in one transfer and scattered on the
+  // device, so launches queued after this call on `stream` see the new
+  // tables and earlier ones the old.  Nothing here waits for the device
+  // unless the staging buffer's copy from two syncs ago is still pending.
   rkv_alloc *a = p->alloc;
-  const size_t W = (size_t)a->d.max_pages_per_seq;
-  bool lens_dirty = false;
-  for (int32_t s = 0; s < a->d.max_seqs; ++s) {
+  const int32_t W = a->d.max_pages_per_seq;
+  const int32_t S = a->d.max_seqs;
+  const uint32_t slot = p->n_syncs & 1u;
+  hipError_t e = hipEventSynchronize(p->stage_done[slot]);
+  if (e != hipSuccess) return hip_fail(op, e);
+  int32_t *h = p->h_stage[slot];
+  int32_t n_rows = 0;
+  for (int32_t s = 0; s < S; ++s) {
     if (!a->dirty[s]) continue;
-    lens_dirty = true;
-    if ((e = hipMemcpy(p->d_tables + s * W, &a->tables[s * W], sizeof(int32_t) * W,
-                       hipMemcpyHostToDevice)) != hipSuccess)
-      return hip_fail(op, e);
+    int32_t *rec = h + (size_t)n_rows * (W + 1);
+    rec[0] = s;
+    std::memcpy(rec + 1, &a->tables[(size_t)s * W], sizeof(int32_t) * W);
     a->dirty[s] = 0;
+    ++n_rows;
   }
-  if (lens_dirty &&
-      (e = hipMemcpy(p->d_lens, a->lens.data(), sizeof(int32_t) * a->lens.size(),
-                     hipMemcpyHostToDevice)) != hipSuccess)
+  std::memcpy(h + (size_t)n_rows * (W + 1), a->lens.data(), sizeof(int32_t) * S);
+  const size_t bytes = sizeof(int32_t) * ((size_t)n_rows * (W + 1) + S);
+  hipStream_t hs = as_stream(stream);
+  if ((e = hipMemcpyAsync(p->d_stage, h, bytes, hipMemcpyHostToDevice, hs)) != hipSuccess)
+    return hip_fail(op, e);
+  if ((e = hipEventRecord(p->stage_done[slot], hs)) != hipSuccess) return hip_fail(op, e);
+  ++p->n_syncs;
+  if ((e = rkv::launch_table_scatter(p->d_stage, n_rows, W, S, p->d_tables, p->d_lens, hs)) !=
+      hipSuccess)
     return hip_fail(op, e);
   return RKV_OK;
 }
