@@ -18,9 +18,9 @@ OBJDIR = os.path.join(HERE, "_build")
 SOURCES = ["rkv_append.hip", "rkv_decode.hip", "rkv_decode_rows32.hip", "rkv_runtime.cpp"]
 
 # Per-file extra flags.  rkv_decode.hip: MFMA destinations and accumulators
-# in VGPRs (no AGPR<->VGPR copies around the VALU work on them); the 32-row
-# variant in rkv_decode_rows32.hip stays on the default allocation (the
-# option crashes the compiler on it).
+# in VGPRs (no AGPR<->VGPR copies around the VALU work on them).  The
+# two-wave 32-row variant (rkv_decode_rows32.hip) is bounded to 256 registers
+# per wave by its launch bounds and allocates no AGPRs either way.
 EXTRA = {"rkv_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 # -packed-fp32-ops off: no v_pk_*_f32 are generated (unreliable on this pool).

@@ -1,8 +1,7 @@
 // rkv_decode_kernel.h -- the paged Q8_0 flash-decode kernel template (GQA,
 // causal multi-query verify, split-K partitions) for gfx950 (CDNA4), shared
-// by rkv_decode.hip (up to 16 rows per kv head) and rkv_decode_rows32.hip
-// (17..32 rows, built without -amdgpu-mfma-vgpr-form, which the compiler
-// cannot apply to that register-heavy variant).
+// by rkv_decode.hip (up to 16 rows per kv head, one wave per workgroup) and
+// rkv_decode_rows32.hip (17..32 rows, two waves per workgroup).
 //
 // Algorithm: the online-softmax flash decode of
 // har/crates/har-serve/src/attention.rs:169-215 (chunked scores, running
@@ -198,8 +197,16 @@ __device__ __forceinline__ T lds_load(const lds_u8 *p) {
 // stays <= 2^kTau and the accumulators are rescaled only a few times.
 constexpr float kTau = 4.0f;
 
-// One workgroup's decode of one (partition, batch entry, kv head).
-template <int D, int NT, bool kSmall, int NS>
+// Workgroup barrier without memory fences: a fenced barrier would also wait
+// for every tile copy in flight.  The explicit vmcnt waits order the copies;
+// the "memory" clobber keeps the compiler from moving LDS accesses across.
+__device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// One wave's share of the decode of one (partition, batch entry, kv head).
+// With NW = 2 waves per workgroup, wave w owns query rows 16w .. 16w+15 and
+// issues every other copy of each tile; the waves share the LDS stages and
+// meet at two barriers per tile (stage free, tile landed).
+template <int D, int NT, bool kSmall, int NS, int NW = 1>
 struct Decoder {
   using S = StageShape<D>;
   static constexpr int NP = (NT + 1) / 2;  // PV n-tiles of 16 rows
@@ -207,7 +214,7 @@ struct Decoder {
   static constexpr int NB = D / 32;        // Q8 blocks per row
 
   const DecodeLaunch &p;
-  int lane, li, lg, kvh, b;
+  int lane, li, lg, kvh, b, wave;
   int32_t seq, len, tok0, tok_end, n_tiles;
   int32_t app_mode;        // 0: no rows to append here; 1: before the first copy; 2: after the prologue copies
   int32_t pg_first;        // first page index (within the sequence) of the partition
@@ -236,6 +243,7 @@ struct Decoder {
       const uint32_t s0 = (uint32_t)(t0 % g.page_tokens);
 #pragma unroll
       for (int k = 0; k < PL::kN16; ++k) {
+        if (NW > 1 && k % NW != wave) continue;
         const uint32_t voff = plan.off[k] + s0 * plan.mul[k];
         __builtin_amdgcn_global_load_lds(base + voff, dst + PL::dst16(k), 16, 0, 0);
       }
@@ -247,11 +255,13 @@ struct Decoder {
       const uint8_t *base1 = kv_base + (uint64_t)pid1 * PB;
 #pragma unroll
       for (int k = 0; k < PL::kN16; ++k) {
+        if (NW > 1 && k % NW != wave) continue;
         const bool h = (plan.halves >> k) & 1u;
         __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[k], dst + PL::dst16(k), 16, 0, 0);
       }
 #pragma unroll
       for (int k = 0; k < PL::kN4; ++k) {
+        if (NW > 1 && (PL::kN16 + k) % NW != wave) continue;
         const bool h = (plan.halves >> (PL::kN16 + k)) & 1u;
         __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[PL::kN16 + k], dst + PL::dst4(k), 4, 0, 0);
       }
@@ -425,9 +435,11 @@ struct Decoder {
   }
 
   // vmcnt wait for the tile about to be computed when `ahead` later tiles'
-  // copies are still in flight (each tile is S::kInstr copies).
+  // copies are still in flight.  A tile is kInstr copies, split over the NW
+  // waves; counting floor(kInstr / NW) per tile is exact for the waves with
+  // that many and waits one copy longer for the others.
   __device__ __forceinline__ static void wait_tiles_ahead(int ahead) {
-    constexpr int kI = ChunkPlan<D, kSmall>::kInstr;
+    constexpr int kI = ChunkPlan<D, kSmall>::kInstr / NW;
     if (ahead >= 2) {
       constexpr int n = 2 * kI;
       __builtin_amdgcn_s_waitcnt(kWaitBase | (n & 0xf) | ((n >> 4) << 14));
@@ -441,9 +453,11 @@ struct Decoder {
 
   // Tile t: prefetch tile t+NS-1 into `fill`, wait for `cur`, compute it.
   __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
+    if (NW > 1) wg_barrier();  // every wave is done with `fill` (tile t-1)
     if (t + NS - 1 < n_tiles) issue(t + NS - 1, fill);
     const int ahead = min(n_tiles - 1 - t, NS - 1);
     wait_tiles_ahead(ahead);
+    if (NW > 1) wg_barrier();  // every wave's copies of tile t have landed
     compute(t, cur);
   }
 
@@ -453,12 +467,17 @@ struct Decoder {
   // vmcnt waits above instead of draining every copy.
   __device__ __forceinline__ void run(lds_u8 *__restrict__ s0, lds_u8 *__restrict__ s1,
                                       lds_u8 *__restrict__ s2) {
-    if (app_mode == 1) append_rows();
+    // appended rows are written by wave 0; the other waves copy their tiles
+    // only after a barrier that follows the stores
+    if (app_mode == 1) {
+      if (wave == 0) append_rows();
+      if (NW > 1) wg_barrier();
+    }
     if (n_tiles > 0) issue(0, s0);
     if constexpr (NS == 3) {
       if (n_tiles > 1) issue(1, s1);
     }
-    if (app_mode == 2) append_rows();
+    if (app_mode == 2 && wave == 0) append_rows();
     if constexpr (NS == 2) {
       int t = 0;
       for (; t + 1 < n_tiles; t += 2) {
@@ -482,8 +501,7 @@ struct Decoder {
 
 // Length of batch entry e, 0 when its sequence id or length is out of range
 // (the entry then has one partition, whose workgroup reports the fault).
-__device__ __forceinline__ int32_t entry_len(const DecodeLaunch &p, int32_t e) {
-  const int32_t sq = p.seq_ids[e];
+__device__ __forceinline__ int32_t entry_len(const DecodeLaunch &p, int32_t sq) {
   if (sq < 0 || sq >= p.n_seqs) return 0;
   const int32_t L = p.seq_lens[sq];
   return (L < 0 || L > p.max_len) ? 0 : L;
@@ -506,56 +524,78 @@ __device__ __forceinline__ int32_t wave_isum(int32_t v, int lane) {
   return __builtin_amdgcn_readlane(wave_iscan(v, lane), 63);
 }
 
-// The partition length of the launch and this workgroup's (entry b,
-// partition part of nb).  Every workgroup computes the same length and the
-// same ordering (entries in batch order, partitions in token order), so
-// workgroup x takes the x-th partition.  Returns false past the last one.
+// The partition length of the launch and this workgroup's entry b (its
+// sequence id and length), partition `part` of nb.  Every workgroup computes
+// the same length and the same order (entries in batch order, partitions in
+// token order), so workgroup x takes the x-th partition.  Returns false past
+// the last one.
 __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t x, int32_t &pt,
-                                       int32_t &b, int32_t &part, int32_t &nb) {
-  constexpr int kCached = 4;  // lengths of entries < 256 stay in registers
-  int32_t lc[kCached];
+                                       int32_t &b, int32_t &seq, int32_t &len, int32_t &part,
+                                       int32_t &nb) {
+  constexpr int kCached = 4;  // entries < 256 stay in registers
+  int32_t lc[kCached], sc[kCached];
 #pragma unroll
   for (int c = 0; c < kCached; ++c) {
     const int32_t e = 64 * c + lane;
-    lc[c] = e < p.batch ? entry_len(p, e) : -1;
+    sc[c] = e < p.batch ? p.seq_ids[e] : -1;
+    lc[c] = e < p.batch ? entry_len(p, sc[c]) : -1;  // -1: no entry
   }
-  auto len_at = [&](int c) -> int32_t {
+  auto len_at = [&](int c, int32_t &sq) -> int32_t {
     if (c < kCached) {
       int32_t v = lc[0];
+      sq = sc[0];
 #pragma unroll
       for (int k = 1; k < kCached; ++k)
-        if (c == k) v = lc[k];
+        if (c == k) {
+          v = lc[k];
+          sq = sc[k];
+        }
       return v;
     }
     const int32_t e = 64 * c + lane;
-    return e < p.batch ? entry_len(p, e) : -1;
+    sq = e < p.batch ? p.seq_ids[e] : -1;
+    return e < p.batch ? entry_len(p, sq) : -1;
   };
   const int n_chunks = (p.batch + 63) / 64;
   pt = p.part_tokens;
   if (pt == 0) {
+    int32_t sq;
     auto count = [&](int32_t t) -> int32_t {
       int32_t tot = 0;
       for (int c = 0; c < n_chunks; ++c) {
-        const int32_t L = len_at(c);
+        const int32_t L = len_at(c, sq);
         tot += wave_isum(L < 0 ? 0 : (L > 0 ? (L + t - 1) / t : 1), lane);
       }
       return tot;
     };
-    int32_t lo = p.pt_kmin, hi = p.pt_kmax;
-    if (count(hi * p.pt_unit) > p.target_parts) {
-      lo = hi;
-    } else {
-      while (lo < hi) {
-        const int32_t mid = (lo + hi) >> 1;
-        if (count(mid * p.pt_unit) <= p.target_parts) hi = mid;
-        else lo = mid + 1;
+    // count(k*unit) >= (sum of ceil(L/unit)) / k, so no k below
+    // ceil(that sum / target) can do: start the search there (exact in one
+    // evaluation when the lengths are equal)
+    int32_t units = 0;
+    for (int c = 0; c < n_chunks; ++c) {
+      const int32_t L = len_at(c, sq);
+      units += wave_isum(L > 0 ? (L + p.pt_unit - 1) / p.pt_unit : 0, lane);
+    }
+    const int32_t k0 = (units + p.target_parts - 1) / p.target_parts;
+    int32_t lo = max(p.pt_kmin, min(k0, p.pt_kmax)), hi = p.pt_kmax;
+    if (count(lo * p.pt_unit) > p.target_parts) {
+      if (count(hi * p.pt_unit) > p.target_parts) {
+        lo = hi;
+      } else {
+        ++lo;
+        while (lo < hi) {
+          const int32_t mid = (lo + hi) >> 1;
+          if (count(mid * p.pt_unit) <= p.target_parts) hi = mid;
+          else lo = mid + 1;
+        }
       }
     }
     pt = lo * p.pt_unit;
   }
   int32_t base = 0;
   for (int c = 0; c < n_chunks; ++c) {
-    const int32_t L = len_at(c);
+    int32_t sq;
+    const int32_t L = len_at(c, sq);
     const int32_t n = L < 0 ? 0 : (L > 0 ? (L + pt - 1) / pt : 1);
     const int32_t cum = wave_iscan(n, lane);
     const uint64_t hit = __ballot(L >= 0 && base + cum > x);
@@ -563,6 +603,8 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
       const int l = __builtin_ctzll(hit);
       b = 64 * c + l;
       nb = __builtin_amdgcn_readlane(n, l);
+      seq = __builtin_amdgcn_readlane(sq, l);
+      len = __builtin_amdgcn_readlane(L, l);
       part = x - (base + __builtin_amdgcn_readlane(cum, l) - nb);
       return true;
     }
@@ -571,17 +613,22 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
   return false;
 }
 
-template <int D, int NT, bool kSmall, int NS>
-__global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
+// NW = 1: one wave per workgroup, NT n-tiles of 8 rows (up to 16 rows).
+// NW = 2: two waves, 16 rows each (NT = 2 per wave, up to 32 rows), two
+// waves per SIMD.
+template <int D, int NT, bool kSmall, int NS, int NW = 1>
+__global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using Dec = Decoder<D, NT, kSmall, NS>;
+  using Dec = Decoder<D, NT, kSmall, NS, NW>;
   using S = StageShape<D>;
   constexpr int NP = Dec::NP;
   constexpr int NC = Dec::NC;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
 
   Dec dc(p);
-  dc.lane = threadIdx.x;
+  dc.lane = threadIdx.x & 63;
+  dc.wave = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
+  const int r0 = 16 * dc.wave;  // first query row of this wave
   dc.li = dc.lane & 15;  // MFMA row/column within a 16-lane group
   dc.lg = dc.lane >> 4;  // MFMA k-group
   const int lane = dc.lane, li = dc.li, lg = dc.lg;
@@ -589,11 +636,11 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   dc.kvh = kvh;
   const Geo g = p.g;
 
-  int32_t pt, b, part, nb;
-  if (!locate(p, lane, (int32_t)blockIdx.x, pt, b, part, nb)) return;
+  int32_t pt, b, seq, lenc, part, nb;
+  if (!locate(p, lane, (int32_t)blockIdx.x, pt, b, seq, lenc, part, nb)) return;
   // the combine finds entry b's partials through the header, written before
   // any check can end this workgroup
-  if (p.ws_hdr != nullptr && kvh == 0 && lane == 0) {
+  if (p.ws_hdr != nullptr && kvh == 0 && threadIdx.x == 0) {
     if (blockIdx.x == 0) p.ws_hdr[0] = pt;
     if (part == 0) {
       p.ws_hdr[1 + 2 * b] = (int32_t)blockIdx.x;
@@ -602,15 +649,15 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   }
   if (p.ws_cnt != nullptr && kvh == 0 && part == 0) {
     const int32_t rows = p.q_len * p.q_heads;
-    for (int32_t r = lane; r < rows; r += 64) p.ws_cnt[(int64_t)b * rows + r] = 0;
+    for (int32_t r = threadIdx.x; r < rows; r += 64 * NW) p.ws_cnt[(int64_t)b * rows + r] = 0;
   }
 
-  const int32_t seq = p.seq_ids[b];
   if (seq < 0 || seq >= p.n_seqs) {
     if (lane == 0) atomicOr(p.fault, FAULT_BAD_SEQ);
     return;
   }
-  const int32_t len = p.seq_lens[seq];
+  // locate() maps an out-of-range length to 0; reread it to tell the two apart
+  const int32_t len = lenc > 0 ? lenc : p.seq_lens[seq];
   if (len < 0 || len > p.bt_stride * g.page_tokens || len > p.max_len) {
     if (lane == 0) atomicOr(p.fault, FAULT_BAD_POSITION);
     return;
@@ -628,7 +675,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   // by the partition that holds their position, before its copies read them
   dc.app_mode = 0;
   if (p.app_k != nullptr) {
-    if (part == 0 && kvh == 0 && lane < p.q_len) {
+    if (part == 0 && kvh == 0 && threadIdx.x < p.q_len) {
       const int32_t row = b * p.q_len + lane;
       const int32_t pos = p.app_pos[row];
       if (p.app_seq_ids[row] != seq) atomicOr(p.fault, FAULT_BAD_SEQ);
@@ -653,7 +700,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   float qmul[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    const int row = 8 * nt + (li & 7);
+    const int row = r0 + 8 * nt + (li & 7);
     float qv[NC][16];
 #pragma unroll
     for (int c = 0; c < NC; ++c)
@@ -722,7 +769,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
   // ---- per-lane softmax rows: PV n-tile np, column li -> row 16*np + li ---
 #pragma unroll
   for (int np = 0; np < NP; ++np) {
-    const int row = 16 * np + li;
+    const int row = r0 + 16 * np + li;
     const int nt = 2 * np + (li >> 3);
     // every lane of column li computed the scale of row 8*nt + (li & 7)
     float mul = 0.0f;
@@ -762,7 +809,7 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
     float l = dc.lrun[np];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
-    const int row = 16 * np + li;
+    const int row = r0 + 16 * np + li;
     if (row >= R) continue;
     const int j = row / q_per_kv;
     const int h = kvh * q_per_kv + row % q_per_kv;
@@ -796,13 +843,13 @@ __global__ __launch_bounds__(64) void decode_kernel(DecodeLaunch p) {
 #endif  // __HIP_DEVICE_COMPILE__
 }
 
-template <int D, int NT, int NS>
+template <int D, int NT, int NS, int NW = 1>
 hipError_t launch_decode_t(const DecodeLaunch &d, hipStream_t s) {
   dim3 grid((unsigned)d.n_wg, (unsigned)d.g.kv_heads);
   if (d.g.page_tokens < kTile)
-    hipLaunchKernelGGL((decode_kernel<D, NT, true, NS>), grid, dim3(64), 0, s, d);
+    hipLaunchKernelGGL((decode_kernel<D, NT, true, NS, NW>), grid, dim3(64 * NW), 0, s, d);
   else
-    hipLaunchKernelGGL((decode_kernel<D, NT, false, NS>), grid, dim3(64), 0, s, d);
+    hipLaunchKernelGGL((decode_kernel<D, NT, false, NS, NW>), grid, dim3(64 * NW), 0, s, d);
   return hipGetLastError();
 }
 
