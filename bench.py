@@ -49,6 +49,8 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--event-every", type=int, default=5,
+                    help="record the per-kernel HIP events on every N-th timed step")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=32768)
@@ -163,24 +165,27 @@ def main() -> int:
     for _ in range(args.warmup):
         step()
     ctx.sync()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    for e in evs:  # create the events (torch creates them at their first record)
+    # kernel durations: HIP events on every `event_every`-th timed step (event
+    # markers cost the stream a few us each, so not on every step)
+    sampled = list(range(0, args.steps, max(args.event_every, 1)))
+    evs = {i: [torch.cuda.Event(enable_timing=True) for _ in range(4)] for i in sampled}
+    for e in evs.values():  # create the events (torch creates them at their first record)
         for x in e:
             x.record(stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(evs[i])
+        step(evs.get(i))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ctx.sync()
     part = int(ws[:4].view(torch.int32).item())  # the partition length the device chose
     n_parts = (L + part - 1) // part
     dec_from = 0 if fused else 1  # the decode launch starts after the append launch
-    t_step = [evs[i][0].elapsed_time(evs[i][3]) * 1e-3 for i in range(args.steps)]
-    t_app = [0.0 if fused else evs[i][0].elapsed_time(evs[i][1]) * 1e-3 for i in range(args.steps)]
-    t_dec = [evs[i][dec_from].elapsed_time(evs[i][2]) * 1e-3 for i in range(args.steps)]
-    t_cmb = [evs[i][2].elapsed_time(evs[i][3]) * 1e-3 for i in range(args.steps)]
+    t_step = [evs[i][0].elapsed_time(evs[i][3]) * 1e-3 for i in sampled]
+    t_app = [0.0 if fused else evs[i][0].elapsed_time(evs[i][1]) * 1e-3 for i in sampled]
+    t_dec = [evs[i][dec_from].elapsed_time(evs[i][2]) * 1e-3 for i in sampled]
+    t_cmb = [evs[i][2].elapsed_time(evs[i][3]) * 1e-3 for i in sampled]
     step_s = wall / args.steps  # whole-job rate over the timed region
     dec_s = sum(t_dec) / len(t_dec)
 
@@ -226,7 +231,8 @@ def main() -> int:
         "kernel_us": {"append": round(1e6 * sum(t_app) / len(t_app), 2),
                       "decode": round(1e6 * dec_s, 2),
                       "combine": round(1e6 * sum(t_cmb) / len(t_cmb), 2),
-                      "event_step": round(1e6 * sum(t_step) / len(t_step), 2)},
+                      "event_step": round(1e6 * sum(t_step) / len(t_step), 2),
+                      "sampled_steps": len(sampled), "sampled_every": args.event_every},
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
         "roofline": {"bound": "hbm", "kernel": "decode_kernel<256,1,false,2>",
@@ -400,17 +406,18 @@ def _time_steps(args, stream, step, n_events=2):
     for i in range(args.warmup):
         step(i, None)
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(n_events)] for _ in range(args.steps)]
-    for e in evs:  # create the events (torch creates them at their first record)
+    sampled = list(range(0, args.steps, max(args.event_every, 1)))
+    evs = {i: [torch.cuda.Event(enable_timing=True) for _ in range(n_events)] for i in sampled}
+    for e in evs.values():  # create the events (torch creates them at their first record)
         for x in e:
             x.record(stream)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+        step(args.warmup + i, evs.get(i))
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
-    dec = sum(e[0].elapsed_time(e[1]) for e in evs) * 1e-3 / args.steps
+    dec = sum(e[0].elapsed_time(e[1]) for e in evs.values()) * 1e-3 / len(evs)
     return wall, dec
 
 
