@@ -56,13 +56,15 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineLaunch c) {
 }
 
 // Flat-layout combine.  Block (row, entry, split) merges partitions
-// [64*split, 64*split + 64) of the entry (from the header the decode wrote):
-// its 256 threads form groups of head_dim/4 threads (4 dims each, float4
-// loads); group g takes partitions g, g + groups, ... eight at a time with
-// all their loads in flight, merged online (running max, rescaled sums),
-// then the groups merge through LDS.  One split writes the output; with
-// more, every split stores its (m, l, o) and the last to arrive merges them.
-// All merges are the chunk combine of attention.rs:205-212 in base 2.
+// [chunk*split, chunk*(split+1)) of the entry (from the header the decode
+// wrote).  Up to 16 partitions: one thread per dimension,
+// all loads in one round, no LDS.  More: groups of head_dim/4 threads (4 dims
+// each, float4 loads), group g taking partitions g, g + groups, ... 16 at a
+// time, merged online (running max, rescaled sums), then the groups merge
+// through LDS.  With one split per row the block writes the output; with
+// more it stores its (m, l, o) and combine_splits_kernel merges the splits in
+// a second launch.  All merges are the chunk combine of attention.rs:205-212
+// in base 2.
 struct Merge {
   float m, l;
   float4 o;
@@ -80,15 +82,32 @@ struct Merge {
   }
 };
 
-__global__ __launch_bounds__(256) void combine_flat_kernel(FlatCombineLaunch c) {
+__device__ __forceinline__ void store_res(const FlatCombineLaunch &c, int64_t oi, float4 res) {
+  if (c.out_bf16) {
+    uint16_t *dst = static_cast<uint16_t *>(c.out) + oi;
+    const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(res.x) | ((uint32_t)f32_to_bf16_rtne(res.y) << 16);
+    const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(res.z) | ((uint32_t)f32_to_bf16_rtne(res.w) << 16);
+    *reinterpret_cast<uint2 *>(dst) = uint2{w0, w1};
+  } else {
+    *reinterpret_cast<float4 *>(static_cast<float *>(c.out) + oi) = res;
+  }
+}
+
+__device__ __forceinline__ void store_row(const FlatCombineLaunch &c, int64_t orow, int dt,
+                                          const Merge &t) {
+  const float inv = t.l > 0.0f ? 1.0f / t.l : 0.0f;
+  const float4 res = t.l > 0.0f ? float4{t.o.x * inv, t.o.y * inv, t.o.z * inv, t.o.w * inv}
+                                : float4{0.f, 0.f, 0.f, 0.f};
+  store_res(c, orow * c.head_dim + 4 * dt, res);
+}
+
+constexpr int kCombineThreads = 256;
+
+__global__ __launch_bounds__(kCombineThreads) void combine_flat_kernel(FlatCombineLaunch c) {
   const int row = blockIdx.x;  // j * q_heads + h
   const int b = blockIdx.y;
   const int split = blockIdx.z;
   const int t = threadIdx.x;
-  const int GS = c.head_dim / 4;  // threads per group
-  const int NG = 256 / GS;        // groups
-  const int grp = t / GS, dt = t % GS;
-  const int rows = c.q_len * c.q_heads;
   const int j = row / c.q_heads, h = row % c.q_heads;
   const int q_per_kv = c.q_heads / c.kv_heads;
   const int kvh = h / q_per_kv;
@@ -97,17 +116,53 @@ __global__ __launch_bounds__(256) void combine_flat_kernel(FlatCombineLaunch c) 
   const int32_t start = c.hdr[1 + 2 * b];
   int32_t n = c.hdr[2 + 2 * b];
   if (start < 0 || n < 1 || start > c.n_wg - n) n = 0;
-  const int32_t n_splits = n > 0 ? (n + kCombineChunk - 1) / kCombineChunk : 1;
+  const int32_t n_splits = n > 0 ? (n + c.chunk - 1) / c.chunk : 1;
   if (split >= n_splits) return;
-  const int32_t i_end = min(n, (split + 1) * kCombineChunk);
+  const int32_t i_beg = split * c.chunk;
+  const int32_t i_end = min(n, i_beg + c.chunk);
   const int64_t p0 = ((int64_t)kvh * c.n_wg + start) * R + r;  // partition i at p0 + i*R
+  const int64_t orow = (int64_t)b * c.q_len * c.q_heads + row;
 
-  Merge mg{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
-  for (int32_t i0 = split * kCombineChunk + grp; i0 < i_end; i0 += 8 * NG) {
-    float2 ml[8];
-    float4 ov[8];
+  if (c.splits == 1 && n <= 16) {
+    // one thread per dimension
+    if (t >= c.head_dim) return;
+    float2 ml[16];
+    float ov[16];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int k = 0; k < 16; ++k) {
+      const bool in = k < n;
+      const int64_t pr = p0 + (int64_t)k * R;
+      ml[k] = in ? *reinterpret_cast<const float2 *>(c.ml + 2 * pr) : float2{-INFINITY, 0.0f};
+      ov[k] = in ? c.o[pr * c.head_dim + t] : 0.0f;
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) M = fmaxf(M, ml[k].x);
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const float w = ml[k].x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml[k].x - M);
+        L += ml[k].y * w;
+        O += ov[k] * w;
+      }
+    }
+    const float res = L > 0.0f ? O / L : 0.0f;
+    const int64_t oi = orow * c.head_dim + t;
+    if (c.out_bf16) static_cast<uint16_t *>(c.out)[oi] = f32_to_bf16_rtne(res);
+    else static_cast<float *>(c.out)[oi] = res;
+    return;
+  }
+
+  const int GS = c.head_dim / 4;          // threads per group
+  const int NG = kCombineThreads / GS;    // groups
+  const int grp = t / GS, dt = t % GS;
+  Merge mg{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
+  for (int32_t i0 = i_beg + grp; i0 < i_end; i0 += 16 * NG) {
+    float2 ml[16];
+    float4 ov[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
       const int32_t i = i0 + k * NG;
       const int64_t pr = p0 + (int64_t)i * R;
       const bool in = i < i_end;
@@ -116,7 +171,7 @@ __global__ __launch_bounds__(256) void combine_flat_kernel(FlatCombineLaunch c) 
                  : float4{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) mg.add(ml[k].x, ml[k].y, ov[k]);
+    for (int k = 0; k < 16; ++k) mg.add(ml[k].x, ml[k].y, ov[k]);
   }
 
   __shared__ float s_m[8], s_l[8];
@@ -130,40 +185,42 @@ __global__ __launch_bounds__(256) void combine_flat_kernel(FlatCombineLaunch c) 
   if (grp != 0) return;
   Merge tot{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
   for (int g = 0; g < NG; ++g) tot.add(s_m[g], s_l[g], s_o[g][dt]);
+  if (c.splits == 1) {
+    store_row(c, orow, dt, tot);
+    return;
+  }
+  if (dt == 0)
+    *reinterpret_cast<float2 *>(c.split_ml + 2 * (orow * c.splits + split)) = float2{tot.m, tot.l};
+  *reinterpret_cast<float4 *>(c.split_o + (orow * c.splits + split) * c.head_dim + 4 * dt) = tot.o;
+}
 
-  const int64_t orow = (int64_t)b * rows + row;
-  if (n_splits > 1) {
-    // publish this split; the last split of the row merges all of them
-    float *sm = c.split_ml + 2 * (orow * c.splits + split);
-    if (dt == 0) *reinterpret_cast<float2 *>(sm) = float2{tot.m, tot.l};
-    *reinterpret_cast<float4 *>(c.split_o + (orow * c.splits + split) * c.head_dim + 4 * dt) = tot.o;
-    __threadfence();
-    // group 0 is (part of) wave 0: lane 0's count reaches the group by a shuffle
-    int last = 0;
-    if (dt == 0) last = atomicAdd(c.cnt + orow, 1) == n_splits - 1;
-    last = __shfl(last, 0);
-    if (!last) return;
-    __threadfence();
-    tot = Merge{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
-    for (int32_t q = 0; q < n_splits; ++q) {
-      const float2 v = *reinterpret_cast<const float2 *>(c.split_ml + 2 * (orow * c.splits + q));
-      const float4 o =
-          *reinterpret_cast<const float4 *>(c.split_o + (orow * c.splits + q) * c.head_dim + 4 * dt);
-      tot.add(v.x, v.y, o);
+// Second level: merge the splits of every (row, entry), head_dim/4 threads.
+__global__ __launch_bounds__(64) void combine_splits_kernel(FlatCombineLaunch c) {
+  const int row = blockIdx.x;
+  const int b = blockIdx.y;
+  const int dt = threadIdx.x;
+  if (dt >= c.head_dim / 4) return;
+  int32_t n = c.hdr[2 + 2 * b];
+  const int32_t start = c.hdr[1 + 2 * b];
+  if (start < 0 || n < 1 || start > c.n_wg - n) n = 0;
+  const int32_t n_splits = n > 0 ? min(c.splits, (n + c.chunk - 1) / c.chunk) : 0;
+  const int64_t orow = (int64_t)b * c.q_len * c.q_heads + row;
+  Merge tot{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
+  for (int32_t q0 = 0; q0 < n_splits; q0 += 8) {
+    float2 ml[8];
+    float4 ov[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const bool in = q0 + k < n_splits;
+      const int64_t sp = orow * c.splits + q0 + k;
+      ml[k] = in ? *reinterpret_cast<const float2 *>(c.split_ml + 2 * sp) : float2{-INFINITY, 0.0f};
+      ov[k] = in ? *reinterpret_cast<const float4 *>(c.split_o + sp * c.head_dim + 4 * dt)
+                 : float4{0.f, 0.f, 0.f, 0.f};
     }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) tot.add(ml[k].x, ml[k].y, ov[k]);
   }
-  const float inv = tot.l > 0.0f ? 1.0f / tot.l : 0.0f;
-  const float4 res = tot.l > 0.0f ? float4{tot.o.x * inv, tot.o.y * inv, tot.o.z * inv, tot.o.w * inv}
-                                  : float4{0.f, 0.f, 0.f, 0.f};
-  const int64_t oi = orow * c.head_dim + 4 * dt;
-  if (c.out_bf16) {
-    uint16_t *dst = static_cast<uint16_t *>(c.out) + oi;
-    const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(res.x) | ((uint32_t)f32_to_bf16_rtne(res.y) << 16);
-    const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(res.z) | ((uint32_t)f32_to_bf16_rtne(res.w) << 16);
-    *reinterpret_cast<uint2 *>(dst) = uint2{w0, w1};
-  } else {
-    *reinterpret_cast<float4 *>(static_cast<float *>(c.out) + oi) = res;
-  }
+  store_row(c, orow, dt, tot);
 }
 
 template <int D, int NS>
@@ -187,9 +244,10 @@ hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s) {
 
 hipError_t launch_combine_flat(const FlatCombineLaunch &c, hipStream_t s) {
   if (c.batch == 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_flat_kernel,
-                     dim3((unsigned)(c.q_len * c.q_heads), (unsigned)c.batch, (unsigned)c.splits),
-                     dim3(256), 0, s, c);
+  const dim3 grid((unsigned)(c.q_len * c.q_heads), (unsigned)c.batch);
+  hipLaunchKernelGGL(combine_flat_kernel, dim3(grid.x, grid.y, (unsigned)c.splits),
+                     dim3(kCombineThreads), 0, s, c);
+  if (c.splits > 1) hipLaunchKernelGGL(combine_splits_kernel, grid, dim3(64), 0, s, c);
   return hipGetLastError();
 }
 

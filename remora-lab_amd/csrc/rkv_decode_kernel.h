@@ -647,10 +647,6 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
       p.ws_hdr[2 + 2 * b] = nb;
     }
   }
-  if (p.ws_cnt != nullptr && kvh == 0 && part == 0) {
-    const int32_t rows = p.q_len * p.q_heads;
-    for (int32_t r = threadIdx.x; r < rows; r += 64 * NW) p.ws_cnt[(int64_t)b * rows + r] = 0;
-  }
 
   if (seq < 0 || seq >= p.n_seqs) {
     if (lane == 0) atomicOr(p.fault, FAULT_BAD_SEQ);

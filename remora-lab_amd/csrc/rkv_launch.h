@@ -70,7 +70,6 @@ struct DecodeLaunch {
   float *ws_ml;
   float *ws_o;
   int32_t *ws_hdr;
-  int32_t *ws_cnt;  // flat layout: [batch][q_len*q_heads] combine counters, zeroed here
   int32_t *fault;
   int32_t stages;  // LDS ring depth: 2 or 3 (tiles in flight = stages - 1)
   // Optional append (app_k == nullptr: none): row b*q_len + j of app_k/app_v
@@ -121,9 +120,9 @@ struct CombineLaunch {
 hipError_t launch_combine(const CombineLaunch &c, hipStream_t s);
 
 // Combine of the flat partials layout written by a decode launch.
-// Blocks (row, entry, split): split s merges partitions [64s, 64s + 64) of
-// the entry; with more than one split the last one to finish merges the
-// splits' results (kept in split_ml / split_o, counted in cnt).
+// Blocks (row, entry, split): split s merges partitions [chunk*s,
+// chunk*(s+1)) of the entry; with more than one split a second kernel merges
+// the splits' results (kept in split_ml / split_o).
 struct FlatCombineLaunch {
   const float *ml;
   const float *o;
@@ -134,14 +133,13 @@ struct FlatCombineLaunch {
   int32_t kv_heads;
   int32_t head_dim;
   int32_t n_wg;
-  int32_t splits;    // grid.z: upper bound of ceil(partitions of an entry / 64)
+  int32_t splits;    // grid.z: upper bound of ceil(partitions of an entry / chunk)
+  int32_t chunk;     // partitions per split
   float *split_ml;   // [batch][rows][splits][2]
   float *split_o;    // [batch][rows][splits][head_dim]
-  int32_t *cnt;      // [batch][rows]
   void *out;
   int32_t out_bf16;
 };
-constexpr int kCombineChunk = 64;
 hipError_t launch_combine_flat(const FlatCombineLaunch &c, hipStream_t s);
 
 }  // namespace rkv

@@ -417,27 +417,40 @@ int32_t batch_rows_per_kv(const rkv_kv_geometry *g, const rkv_decode_args *a) {
 // Flat workspace of rkv_decode_q8, each part 256-byte aligned:
 //   header   int32 [1 + 2*batch]: partition length; first partition and
 //            partition count of every entry (written by the decode)
-//   counters int32 [batch][q_len*q_heads] of the combine's splits (zeroed by
-//            the decode)
 //   partials f32 (m, l) then o of every (kv head, partition, row)
 //   splits   f32 (m, l) then o of every (entry, row, combine split)
-// so the workspace needs no initialisation.
+// Everything is written before it is read in the same call, so the
+// workspace needs no initialisation.
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 struct WsLayout {
-  size_t hdr = 0, cnt = 0, ml = 0, o = 0, sml = 0, so = 0, total = 0;
-  int32_t splits = 1;
+  size_t hdr = 0, ml = 0, o = 0, sml = 0, so = 0, total = 0;
+  int32_t splits = 1, chunk = 1;
 };
 WsLayout ws_layout(const rkv_kv_geometry *g, const rkv_decode_args *a, const Plan &pl) {
   WsLayout w;
   const size_t B = (size_t)std::max<int32_t>(a->batch, 0);
   const size_t out_rows = B * a->q_len * a->q_heads;
   const size_t prows = (size_t)g->kv_heads * pl.n_wg * batch_rows_per_kv(g, a);
-  // an entry has at most min(n_wg, ceil(max_len / shortest partition)) partitions
+  // partitions of one entry: ceil(max_len / shortest partition), and with a
+  // device-chosen length no more than the target minus one per other entry
+  // (or the count at the longest length, where the search stops)
   const int64_t shortest = pl.pt > 0 ? pl.pt : (int64_t)pl.kmin * pl.unit;
-  const int64_t n_entry = std::min<int64_t>(pl.n_wg, (pl.max_len + shortest - 1) / shortest);
-  w.splits = (int32_t)std::max<int64_t>(1, (n_entry + rkv::kCombineChunk - 1) / rkv::kCombineChunk);
-  w.cnt = align256(sizeof(int32_t) * (1 + 2 * B));
-  w.ml = w.cnt + align256(sizeof(int32_t) * out_rows);
+  int64_t n_entry = (pl.max_len + shortest - 1) / shortest;
+  if (pl.pt == 0) {
+    const int64_t longest = (int64_t)pl.kmax * pl.unit;
+    const int64_t by_target = (int64_t)pl.target - std::max<int64_t>((int64_t)B - 1, 0);
+    n_entry = std::min(n_entry, std::max(by_target, (pl.max_len + longest - 1) / longest));
+  }
+  n_entry = std::min<int64_t>(n_entry, pl.n_wg);
+  // Combine splits: enough (row, entry, split) blocks to keep ~256 CUs busy
+  // when the batch has few rows, else one split per row; a split holds at
+  // least 16 partitions.
+  const int64_t blocks = std::max<int64_t>(1, (int64_t)out_rows);
+  const int64_t want = std::max<int64_t>(1, (256 + blocks - 1) / blocks);
+  const int64_t max_splits = std::max<int64_t>(1, (n_entry + 15) / 16);
+  w.splits = (int32_t)std::min(want, max_splits);
+  w.chunk = (int32_t)std::max<int64_t>(1, (n_entry + w.splits - 1) / w.splits);
+  w.ml = align256(sizeof(int32_t) * (1 + 2 * B));
   w.o = w.ml + align256(sizeof(float) * 2 * prows);
   w.sml = w.o + align256(sizeof(float) * prows * g->head_dim);
   w.so = w.sml + align256(sizeof(float) * 2 * out_rows * w.splits);
@@ -567,7 +580,6 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
     const WsLayout w = ws_layout(g, a, pl);
     uint8_t *base = static_cast<uint8_t *>(a->workspace);
     d.ws_hdr = reinterpret_cast<int32_t *>(base + w.hdr);
-    d.ws_cnt = reinterpret_cast<int32_t *>(base + w.cnt);
     d.ws_ml = reinterpret_cast<float *>(base + w.ml);
     d.ws_o = reinterpret_cast<float *>(base + w.o);
   }
@@ -579,9 +591,9 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
     const WsLayout w = ws_layout(g, a, pl);
     uint8_t *base = static_cast<uint8_t *>(a->workspace);
     rkv::FlatCombineLaunch c{d.ws_ml, d.ws_o, d.ws_hdr, a->batch, a->q_len, a->q_heads,
-                             g->kv_heads, g->head_dim, pl.n_wg, w.splits,
+                             g->kv_heads, g->head_dim, pl.n_wg, w.splits, w.chunk,
                              reinterpret_cast<float *>(base + w.sml),
-                             reinterpret_cast<float *>(base + w.so), d.ws_cnt, a->out, d.out_bf16};
+                             reinterpret_cast<float *>(base + w.so), a->out, d.out_bf16};
     if ((e = rkv::launch_combine_flat(c, hs)) != hipSuccess) return hip_fail(op, e);
   }
   return RKV_OK;
