@@ -267,20 +267,23 @@ def read_traffic():
 
 
 def cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv, D, scale, step_bytes,
-                 n_sample):
+                 n_sample, n_sample_all=16):
     """Time the reference CPU path (oracle/rkv_oracle.c: q8 quantize for the
-    append rows, flash_decode_reference over each sampled sequence) and scale
-    the sample to a whole step.  Also checks those sequences' GPU outputs."""
+    append rows, flash_decode_reference over sampled sequences) and scale the
+    sample to a whole step: on one core (the reference is single-threaded) and
+    on all host cores (OpenMP over sequence x q head).  Also checks those
+    sequences' GPU outputs."""
     import numpy as np
     import torch
     sys.path.insert(0, ROOT)
     from oracle import rko
     rko.lib()
     n_sample = min(n_sample, B)
+    n_all = min(max(n_sample_all, n_sample), B)
     rb = D // 32 * 34
     # host copies of the sampled sequences' rows (reference contiguous layout)
     rows = []
-    for s in range(n_sample):
+    for s in range(n_all):
         kk = torch.empty(Hkv * L * rb, dtype=torch.uint8, device="cuda")
         vv = torch.empty_like(kk)
         pool.gather(0, s, rkv.K, kk)
@@ -298,19 +301,30 @@ def cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv, D, scal
             rko.q8_encode(vn[b, h])
     t_app = time.perf_counter() - t0
     p = rko.fd_params(Hq, Hkv, L, 1024, D)
+    qs = (qf[:n_all, 0] * np.float32(scale)).astype(np.float32)
     max_err = 0.0
     t0 = time.perf_counter()
     for s in range(n_sample):
-        qs = (qf[s, 0] * np.float32(scale)).astype(np.float32).reshape(-1)
-        ref = rko.flash_decode_reference(p, rows[s][0], rows[s][1], qs)
+        ref = rko.flash_decode_reference(p, rows[s][0], rows[s][1], qs[s].reshape(-1))
         max_err = max(max_err, float(np.max(np.abs(ref - gpu_out[s, 0].reshape(-1)))))
     t_dec = time.perf_counter() - t0
     full = t_app + t_dec * B / n_sample
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    t0 = time.perf_counter()
+    many = rko.flash_decode_reference_many(p, [r[0] for r in rows], [r[1] for r in rows], qs, threads)
+    t_many = time.perf_counter() - t0
+    max_err = max(max_err, float(np.max(np.abs(many - gpu_out[:n_all, 0]))))
+    full_all = t_app + t_many * B / n_all
     return {"value": round(step_bytes / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"append quantize of all {B} rows + flash_decode_reference (attention.rs:148-215, "
                       f"chunk 1024) over {n_sample} of {B} sequences at L={L}, scaled x{B / n_sample:g}; "
                       f"{t_app + t_dec:.1f} s of CPU work",
             "us_per_step": round(full * 1e6, 1),
+            "all_cores": {"value": round(step_bytes / full_all / 1e9, 4), "unit": "GB/s",
+                          "cores": threads, "us_per_step": round(full_all * 1e6, 1),
+                          "sample": f"the same loop over {n_all} of {B} sequences on {threads} OpenMP "
+                                    f"threads (sequence x q head), scaled x{B / n_all:g}; "
+                                    f"{t_many:.1f} s wall"},
             "gpu_vs_cpu_max_abs_err_on_sample": max_err}
 
 

@@ -81,6 +81,8 @@ def _declare(L):
         "rko_row_to_words": (None, [P, C.c_size_t, P]),
         "rko_flash_decode_online": (None, [C.POINTER(FdParams), P, P, P, C.c_int32, P, P, P]),
         "rko_flash_decode_reference": (None, [C.POINTER(FdParams), P, P, P, P]),
+        "rko_flash_decode_reference_many": (None, [C.POINTER(FdParams), C.c_int32, P, P, P, P,
+                                                   C.c_int32]),
         "rko_flash_decode_bruteforce": (None, [C.POINTER(FdParams), P, P, P, C.c_int32, P]),
         "rko_flash_decode_partials": (C.c_int32, [C.POINTER(FdParams), P, P, P, C.c_int32, P, P, P]),
         "rko_lse_combine": (None, [C.c_int32, C.c_int32, P, P, P, P, P, P]),
@@ -203,6 +205,21 @@ def flash_decode_reference(p: FdParams, k_words, v_words, query) -> np.ndarray:
     query = np.ascontiguousarray(query, np.float32)
     out = np.empty(p.q_heads * p.head_dim, np.float32)
     lib().rko_flash_decode_reference(C.byref(p), _p(k_words), _p(v_words), _p(query), _p(out))
+    return out
+
+
+def flash_decode_reference_many(p: FdParams, k_words: list, v_words: list, queries,
+                                threads: int) -> np.ndarray:
+    """flash_decode_reference over len(k_words) sequences of p.seq_len tokens
+    on `threads` OpenMP threads; queries [n][q_heads][D] -> out [n][q_heads][D]."""
+    n = len(k_words)
+    queries = np.ascontiguousarray(queries, np.float32)
+    ks = [np.ascontiguousarray(k, np.uint32) for k in k_words]
+    vs = [np.ascontiguousarray(v, np.uint32) for v in v_words]
+    kp = (P * n)(*[_p(k) for k in ks])
+    vp = (P * n)(*[_p(v) for v in vs])
+    out = np.empty((n, p.q_heads, p.head_dim), np.float32)
+    lib().rko_flash_decode_reference_many(C.byref(p), n, kp, vp, _p(queries), _p(out), threads)
     return out
 
 

@@ -437,6 +437,29 @@ void rko_flash_decode_reference(const rko_fd_params *p, const uint32_t *k_words,
   free(o);
 }
 
+/* The reference loop above over n independent sequences (each with its own
+ * contiguous K/V words and q_heads query rows), spread over `threads` OpenMP
+ * threads by (sequence, q head); each head runs attention.rs:148-165
+ * unchanged.  Used to time the CPU path on all host cores. */
+void rko_flash_decode_reference_many(const rko_fd_params *p, int32_t n,
+                                     const uint32_t *const *k_words,
+                                     const uint32_t *const *v_words, const float *queries,
+                                     float *out, int32_t threads) {
+  const int32_t D = p->head_dim;
+  const int32_t q_per_kv = p->q_heads / p->kv_heads;
+  const int32_t total = n * p->q_heads;
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 1)
+  for (int32_t w = 0; w < total; ++w) {
+    const int32_t s = w / p->q_heads, qh = w % p->q_heads;
+    float *o = (float *)malloc(sizeof(float) * (size_t)D);
+    float m, l;
+    rko_flash_decode_online(p, k_words[s], v_words[s], queries + ((size_t)s * p->q_heads + qh) * D,
+                            qh / q_per_kv, &m, &l, o);
+    for (int32_t i = 0; i < D; ++i) out[((size_t)s * p->q_heads + qh) * D + i] = o[i] / l;
+    free(o);
+  }
+}
+
 /* har/crates/har-serve/src/attention.rs:219-250 */
 void rko_flash_decode_bruteforce(const rko_fd_params *p, const uint32_t *k_words,
                                  const uint32_t *v_words, const float *q,

@@ -99,6 +99,12 @@ void rko_flash_decode_online(const rko_fd_params *p, const uint32_t *k_words,
 void rko_flash_decode_reference(const rko_fd_params *p, const uint32_t *k_words,
                                 const uint32_t *v_words, const float *query,
                                 float *out);
+/* rko_flash_decode_reference over n sequences on `threads` OpenMP threads
+ * (by sequence and q head); for timing the CPU path on all host cores */
+void rko_flash_decode_reference_many(const rko_fd_params *p, int32_t n,
+                                     const uint32_t *const *k_words,
+                                     const uint32_t *const *v_words, const float *queries,
+                                     float *out, int32_t threads);
 /* attention.rs:219-250 */
 void rko_flash_decode_bruteforce(const rko_fd_params *p, const uint32_t *k_words,
                                  const uint32_t *v_words, const float *q,

@@ -700,6 +700,93 @@ def test_pool_async_table_updates(rkv, rko, ctx):
     pool.close()
 
 
+def test_continuous_batching_steps(rkv, rko, ctx):
+    """Config 4's flow at a small size on 2 layer pools with 16-token pages:
+    per step some sequences finish (pages freed, restart empty), two append a
+    40-row prefill chunk, the rest decode one token appended inside the decode
+    launch; one stream-ordered table upload per step, no host sync until the
+    end.  Every (step, layer) decode output equals the oracle over that
+    layer's rows at that step."""
+    torch = _torch()
+    Hkv, D, PT, Hq, S, layers = 2, 128, 16, 8, 8, 2
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, 400, S, 48, seed=11)
+    rng = np.random.default_rng(31)
+    rows = [[np.zeros((0, Hkv, D), np.float32) for _ in range(S)] for _ in range(layers)]
+
+    def append(layer, seqs, starts, new, stream=None):
+        sid = np.concatenate([np.full(len(x), s, np.int32) for s, x in zip(seqs, new)])
+        pos = np.concatenate([np.arange(st, st + len(x), dtype=np.int32) for st, x in zip(starts, new)])
+        kv = np.concatenate(new)
+        pool.append(layer, torch.from_numpy(sid).cuda(), torch.from_numpy(pos).cuda(),
+                    torch.from_numpy(kv).cuda(), torch.from_numpy(kv).cuda(), stream=stream)
+
+    lens = [int(x) for x in rng.integers(5, 200, S)]
+    for s in range(S):
+        pool.alloc.reserve(s, lens[s])
+    pool.sync_tables()
+    for layer in range(layers):
+        new = [rng.standard_normal((lens[s], Hkv, D)).astype(np.float32) for s in range(S)]
+        append(layer, range(S), [0] * S, new)
+        for s in range(S):
+            rows[layer][s] = new[s]
+    ctx.sync()
+    stream = torch.cuda.current_stream()
+    keep = []  # device inputs of queued launches
+    checks = []
+    for step in range(4):
+        for s in range(S):
+            if rng.random() < 0.25:
+                pool.alloc.free(s)
+                lens[s] = 0
+                for layer in range(layers):
+                    rows[layer][s] = rows[layer][s][:0]
+        pf = [(2 * step) % S, (2 * step + 1) % S]
+        dset = [s for s in range(S) if s not in pf]
+        for s in pf:
+            pool.alloc.reserve(s, lens[s] + 40)
+        for s in dset:
+            pool.alloc.reserve(s, lens[s] + 1)
+        pool.sync_tables(stream)
+        sid = torch.tensor(dset, dtype=torch.int32, device="cuda")
+        pos = torch.tensor([lens[s] for s in dset], dtype=torch.int32, device="cuda")
+        for layer in range(layers):
+            chunk = [rng.standard_normal((40, Hkv, D)).astype(np.float32) for _ in pf]
+            append(layer, pf, [lens[s] for s in pf], chunk, stream)
+            new = rng.standard_normal((len(dset), Hkv, D)).astype(np.float32)
+            kn = torch.from_numpy(new).cuda()
+            q = torch.from_numpy(rng.standard_normal((len(dset), 1, Hq, D)).astype(np.float32)).cuda()
+            out = torch.empty_like(q)
+            app = rkv.append_args(sid, pos, kn, kn)
+            a = rkv.decode_args(q, out, sid, 0.1, 48 * PT)
+            ws = torch.empty(rkv.decode_workspace_bytes(pool.geometry, a), dtype=torch.uint8, device="cuda")
+            a = rkv.decode_args(q, out, sid, 0.1, 48 * PT, workspace=ws, append=app)
+            pool.decode(layer, a, stream=stream)
+            keep.append((kn, q, ws, app, a))
+            for i, s in enumerate(pf):
+                rows[layer][s] = np.concatenate([rows[layer][s], chunk[i]])
+            for i, s in enumerate(dset):
+                rows[layer][s] = np.concatenate([rows[layer][s], new[i:i + 1]])
+            checks.append((step, layer, out, q,
+                           {s: rows[layer][s].copy() for s in dset}, list(dset)))
+        for s in pf:
+            lens[s] += 40
+        for s in dset:
+            lens[s] += 1
+    ctx.sync()
+    for step, layer, out, q, snap, dset in checks:
+        got = out.cpu().numpy()
+        qn = q.cpu().numpy()
+        for i, s in enumerate(dset):
+            r = snap[s]
+            kq = np.stack([rko.q8_encode(r[t, h]) for t in range(len(r)) for h in range(Hkv)])
+            kq = kq.reshape(len(r), Hkv, -1).transpose(1, 0, 2).copy()
+            p = rko.fd_params(Hq, Hkv, len(r), 1024, D)
+            want = rko.flash_decode_reference(p, rko.rows_to_words(kq), rko.rows_to_words(kq),
+                                              (qn[i, 0] * np.float32(0.1)).astype(np.float32).reshape(-1))
+            assert_close(got[i, 0].reshape(-1), want, what=f"step {step} layer {layer} seq {s}")
+    pool.close()
+
+
 def _as_u8(ptr, n):
     """A uint8 torch view of n bytes of device memory owned by the pool."""
     torch = _torch()

@@ -266,6 +266,22 @@ def test_online_matches_bruteforce(rko):
         assert np.all(np.abs(o / l - bf) < 1e-5)
 
 
+def test_reference_many_equals_reference(rko):
+    """The multi-threaded timing helper runs the same per-head loop: bit-equal
+    to flash_decode_reference for every sequence."""
+    p = rko.fd_params(8, 2, 300, 128, 256)
+    ks, vs, qs = [], [], []
+    for s in range(3):
+        kw, vw = _kv_cache(rko, p, 50 + s)
+        ks.append(kw)
+        vs.append(vw)
+        qs.append(rko.lcg_values(8 * 256, 90 + s).reshape(8, 256))
+    got = rko.flash_decode_reference_many(p, ks, vs, np.stack(qs), threads=4)
+    for s in range(3):
+        want = rko.flash_decode_reference(p, ks[s], vs[s], qs[s].reshape(-1))
+        assert np.array_equal(got[s].reshape(-1), want)
+
+
 def test_gqa_mapping_uses_shared_kv_head(rko):
     """attention.rs:320-342."""
     p = rko.fd_params(4, 2, 64, 32)
