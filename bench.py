@@ -60,7 +60,8 @@ def parse():
     ap.add_argument("--page-size", type=int, default=64)
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--config", type=int, default=1,
-                    help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs")
+                    help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs; "
+                         "6 = prefix-shared decode (forks + copy-on-write pages)")
     ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
     ap.add_argument("--append-launch", action="store_true",
                     help="append the step's rows with a separate rkv_pool_append launch instead "
@@ -235,7 +236,7 @@ def main() -> int:
                       "sampled_steps": len(sampled), "sampled_every": args.event_every},
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
-        "roofline": {"bound": "hbm", "kernel": "decode_kernel<256,1,false,2>",
+        "roofline": {"bound": "hbm", "kernel": "rkv::decode_kernel<256, 1, false, 2, 1>",
                      "achieved": round(dec_bytes / dec_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(), "algorithmic_bytes_per_launch": dec_bytes},
@@ -657,10 +658,107 @@ def run_config4(args) -> int:
     return 0
 
 
+def run_config6(args) -> int:
+    """Prefix sharing: 64 sequences forked from one 30752-token prefix (it
+    ends inside a page) each grow a private suffix to L=32768, so every
+    child's first suffix row lands in a copy-on-write copy of the prefix's
+    last page.  The parent is then freed; its pages live on through the
+    children's references.  Set-up times the table sync that runs the
+    64 x layers page copies.  Each step is the headline's decode (one row
+    appended per sequence inside the launch) over the children, rotating over
+    4 layer pools.  `value` counts the logical K/V bytes the decode serves;
+    the prefix is stored once, so `unique_kv_bytes` is far smaller and most
+    reads hit the caches."""
+    import numpy as np
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    Hq, Hkv, D, PT = 16, 2, 256, 64
+    B, layers, L, prefix = 64, 4, 32768, 30752
+    pps = L // PT
+    unique_pages = (prefix + PT - 1) // PT + B * ((L - prefix + PT - 1) // PT + 1)
+    num_pages = int(math.ceil(unique_pages * 1.10))
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, num_pages, B + 1, pps, seed=args.seed)
+    parent = B
+    pool.alloc.reserve(parent, prefix)
+    pool.sync_tables()
+    for layer in range(layers):
+        _fill_layer(rkv, pool, layer, [parent], [prefix], Hkv, D, args.seed)
+    for s in range(B):
+        pool.alloc.fork(parent, s, prefix)
+    pool.alloc.free(parent)
+    for s in range(B):
+        pool.alloc.reserve(s, L)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    pool.sync_tables(stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    cow_us = e0.elapsed_time(e1) * 1e3
+    page_b = rkv.page_bytes(pool.geometry)
+    cow_bytes = 2 * B * layers * page_b
+    for layer in range(layers):
+        suffix_pos = np.arange(prefix, L, dtype=np.int32)
+        sid = np.repeat(np.arange(B, dtype=np.int32), L - prefix)
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(2000 + layer + args.seed)
+        for a in range(0, len(sid), 1 << 16):
+            n = min(1 << 16, len(sid) - a)
+            k = torch.randn((n, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+            v = torch.randn((n, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+            pos = torch.from_numpy(np.tile(suffix_pos, B)[a:a + n]).to(dev)
+            pool.append(layer, torch.from_numpy(sid[a:a + n]).to(dev), pos, k, v)
+    ctx.sync()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 5)
+    seq_ids = torch.arange(B, device=dev, dtype=torch.int32)
+    positions = torch.full((B,), L - 1, device=dev, dtype=torch.int32)
+    k_new = torch.randn((B, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((B, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((B, 1, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty((B, 1, Hq, D), device=dev, dtype=torch.float32)
+    app = rkv.append_args(seq_ids, positions, k_new, v_new)
+    dec = _Decoder(rkv, ctx, pool, q, out, seq_ids, 1.0 / math.sqrt(D), L, 1, app,
+                   args.partition_tokens, stream)
+
+    def step(i, ev):
+        dec(i % layers, ev)
+
+    wall, dec_s = _time_steps(args, stream, step)
+    ctx.sync()
+    row = D // 32 * 34
+    kv = B * L * Hkv * 2 * row
+    unique_kv = (prefix + B * (L - prefix)) * Hkv * 2 * row
+    step_bytes = kv + B * Hq * D * (2 + 4) + B * pps * 4 + B * Hkv * 2 * (D * 2 + row)
+    flops = 4 * D * Hq * B * L
+    _line(args, 6, (f"prefix-shared decode: B={B} sequences forked from one {prefix}-token prefix, "
+                    f"private suffixes to L={L}, Hq=16, Hkv=2, D=256, page 64, one row appended "
+                    f"per sequence in the decode launch, {layers} rotating layer pools"),
+          wall, None, step_bytes, step_bytes, flops,
+          {"config": {"batch": B, "layers_rotated": layers, "prefix_tokens": prefix,
+                      "partition_tokens": dec.partition_tokens(),
+                      "pool_pages_per_layer": num_pages},
+           "unique_kv_bytes": unique_kv,
+           "unique_kv_gbs": round(unique_kv / wall / 1e9, 2),
+           "decode_us": round(dec_s * 1e6, 2),
+           "cow_sync": {"pairs": B, "layers": layers, "us": round(cow_us, 2),
+                        "page_bytes_moved": cow_bytes,
+                        "gbs": round(cow_bytes / (cow_us * 1e-6) / 1e9, 2)}})
+    pool.close()
+    ctx.close()
+    return 0
+
+
 if __name__ == "__main__":
     _a = parse()
     if _a.config == 4:
         sys.exit(run_config4(_a))
+    if _a.config == 6:
+        sys.exit(run_config6(_a))
     if _a.config in (2, 3, 5):
         sys.exit(run_config(_a))
     sys.exit(main())

@@ -119,6 +119,29 @@ rkv_status rkv_alloc_free_pages(const rkv_alloc *a, int32_t *n);
  * lengths [max_seqs] to host buffers. */
 rkv_status rkv_alloc_export(const rkv_alloc *a, int32_t *tables, int32_t *lens);
 
+/* Prefix sharing.  The reference shares prefix pages logically: a lease
+ * raises a page's reference_count and eviction refuses referenced pages
+ * (har-kv/src/graph.rs:447-533).  Here the sharing is physical: every page
+ * carries the number of block-table entries naming it and returns to the
+ * free list when that drops to zero.
+ *
+ * rkv_seq_fork: the empty sequence `dst` takes the first
+ * ceil(len/page_tokens) pages of `src` (0 <= len <= length of src) and has
+ * length len.  Fork after src's rows below len are written (stream order).
+ * Shared pages are read-only and always form a prefix of each table; rows
+ * may be written only at positions a reserve added.  When a reserve grows a
+ * sequence whose partly filled last page is shared, that sequence gets a
+ * fresh page and a queued copy of the shared one (copy-on-write). */
+rkv_status rkv_seq_fork(rkv_alloc *a, int32_t src, int32_t dst, int32_t len);
+/* Block-table entries naming `page` (0 = free). */
+rkv_status rkv_page_refs(const rkv_alloc *a, int32_t page, int32_t *refs);
+/* Move the queued copy-on-write copies, as (src, dst) page pairs, to
+ * `pairs` (host, room for `cap` pairs); *n = number queued.  The copies are
+ * independent of each other.  Run them (rkv_copy_pages) on the stream before
+ * the next launch that reads or writes the pages.  A pool does this itself
+ * in rkv_pool_sync_tables. */
+rkv_status rkv_alloc_take_copies(rkv_alloc *a, int32_t *pairs, int32_t cap, int32_t *n);
+
 /* ---- operation arguments -------------------------------------------------- */
 typedef struct rkv_append_args {
   int32_t n_rows;
@@ -227,6 +250,16 @@ rkv_status rkv_import_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
                          const int32_t *block_table, int32_t len, int32_t kind,
                          const uint8_t *rows, void *stream);
 
+/* Copy-on-write page copies: page dst := page src for each (src, dst) pair
+ * of `pairs` (device, n_pairs pairs), in each of `layers` page arrays
+ * starting layer_stride_bytes apart at `pages`.  No reference counterpart:
+ * the reference never copies a KV page (har-kv/src/graph.rs:447-533 shares
+ * them only logically).  Pairs naming pages outside [0, num_pages) are
+ * skipped. */
+rkv_status rkv_copy_pages(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
+                          int64_t layer_stride_bytes, int32_t layers,
+                          const int32_t *pairs, int32_t n_pairs, void *stream);
+
 /* Batch f32 -> binary16 bits with the device encoder of one rule
  * (RKV_Q8_CANONICAL = r4kv/src/f16.rs:27-86, RKV_Q8_HARSERVE =
  * attention.rs:45-76); used to pin the scale encoder over many inputs. */
@@ -269,11 +302,13 @@ typedef struct rkv_pool rkv_pool;
 rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **out);
 rkv_status rkv_pool_destroy(rkv_pool *pool);
 rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
-/* Upload the allocator's changed block-table rows and all lengths, ordered
- * on `stream`: launches enqueued on `stream` afterwards see the new tables,
- * earlier ones the old.  One pinned-staging copy plus one small kernel; the
- * host waits only if the staging buffer of the call before last is still in
- * flight.  Use one stream for a pool's syncs and launches. */
+/* Upload the allocator's changed block-table rows and all lengths and run
+ * its queued copy-on-write page copies (all layers), ordered on `stream`:
+ * launches enqueued on `stream` afterwards see the new tables and copied
+ * pages, earlier ones the old.  One pinned-staging copy plus one or two
+ * small kernels; the host waits only if the staging buffer of the call
+ * before last is still in flight.  Use one stream for a pool's syncs and
+ * launches. */
 rkv_status rkv_pool_sync_tables(rkv_pool *pool, void *stream);
 /* Device pointers owned by the pool. */
 void *rkv_pool_layer_pages(rkv_pool *pool, int32_t layer);

@@ -95,6 +95,11 @@ _SIGS = {
     "rkv_block_table_get": (C.c_int32, [P, C.c_int32, I32P, C.c_int32, I32P]),
     "rkv_alloc_free_pages": (C.c_int32, [P, I32P]),
     "rkv_alloc_export": (C.c_int32, [P, P, P]),
+    "rkv_seq_fork": (C.c_int32, [P, C.c_int32, C.c_int32, C.c_int32]),
+    "rkv_page_refs": (C.c_int32, [P, C.c_int32, I32P]),
+    "rkv_alloc_take_copies": (C.c_int32, [P, P, C.c_int32, I32P]),
+    "rkv_copy_pages": (C.c_int32, [P, C.POINTER(Geometry), P, C.c_int64, C.c_int32, P,
+                                   C.c_int32, P]),
     "rkv_append_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32,
                                   C.POINTER(AppendArgs), P]),
     "rkv_decode_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P, C.c_int32,
@@ -218,6 +223,7 @@ class Allocator:
             check(lib().rkv_alloc_create(C.byref(d), C.byref(h)))
             handle = h
         self.h = handle
+        self.num_pages = num_pages
         self.max_seqs = max_seqs
         self.max_pages_per_seq = max_pages_per_seq
 
@@ -229,6 +235,22 @@ class Allocator:
 
     def free(self, seq: int) -> None:
         check(lib().rkv_seq_free(self.h, seq))
+
+    def fork(self, src: int, dst: int, length: int) -> None:
+        """Share src's first `length` tokens with the empty sequence dst."""
+        check(lib().rkv_seq_fork(self.h, src, dst, length))
+
+    def page_refs(self, page: int) -> int:
+        n = C.c_int32()
+        check(lib().rkv_page_refs(self.h, page, C.byref(n)))
+        return n.value
+
+    def take_copies(self) -> list[tuple[int, int]]:
+        """Queued copy-on-write copies as (src, dst) pairs; clears the queue."""
+        buf = (C.c_int32 * (2 * self.num_pages))()
+        n = C.c_int32()
+        check(lib().rkv_alloc_take_copies(self.h, buf, self.num_pages, C.byref(n)))
+        return [(buf[2 * i], buf[2 * i + 1]) for i in range(n.value)]
 
     def seq_len(self, seq: int) -> int:
         n = C.c_int32()
@@ -350,6 +372,13 @@ def import_q8(ctx: Ctx, g: Geometry, pages, block_table, length: int, kind: int,
               stream=None) -> None:
     check(lib().rkv_import_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_table), length, kind,
                               _ptr(rows), _stream(stream)))
+
+
+def copy_pages(ctx: Ctx, g: Geometry, pages, layer_stride: int, layers: int, pairs,
+               n_pairs: int, stream=None) -> None:
+    """Page dst := page src per (src, dst) pair of the int32 device tensor `pairs`."""
+    check(lib().rkv_copy_pages(ctx.h, C.byref(g), _ptr(pages), layer_stride, layers,
+                               _ptr(pairs), n_pairs, _stream(stream)))
 
 
 def f32_to_f16(ctx: Ctx, x, out, rule: int, stream=None) -> None:

@@ -5,6 +5,8 @@
 // Quantization rules (bit-exact with the CPU reference): q8_quantize_lane
 // in rkv_device.h -- canonical (har/crates/r4kv/src/quant.rs:45-90) or
 // har-serve (har/crates/har-serve/src/attention.rs:25-42).
+#include <algorithm>
+
 #include "rkv_launch.h"
 
 namespace rkv {
@@ -163,7 +165,55 @@ __global__ __launch_bounds__(256) void table_scatter_kernel(const int32_t *packe
     for (int32_t i = threadIdx.x; i < n_seqs; i += 256) lens[i] = src[i];
   }
 }
+
+// Copy-on-write page copies: for each (src, dst) pair and each of `layers`
+// layer arrays, page dst := page src.  A unit is one 16 KiB piece of one
+// (pair, layer) page; each block walks units with a grid stride and each
+// thread moves four 16-byte vectors per unit, all loads issued before the
+// stores.  Pairs naming pages outside [0, num_pages) are skipped.
+constexpr int32_t kCopyVecs = 4;
+constexpr int32_t kCopyUnitBytes = 256 * 16 * kCopyVecs;
+
+__global__ __launch_bounds__(256) void copy_pages_kernel(uint8_t *pages, int64_t layer_stride,
+                                                         int32_t layers, int32_t num_pages,
+                                                         const int32_t *pairs, int64_t page_bytes,
+                                                         int32_t units_per_page, int64_t n_units) {
+  for (int64_t u = blockIdx.x; u < n_units; u += gridDim.x) {
+    const int64_t pl = u / units_per_page;
+    const int32_t part = (int32_t)(u - pl * units_per_page);
+    const int32_t layer = (int32_t)(pl % layers);
+    const int64_t pair = pl / layers;
+    const int32_t src = pairs[2 * pair], dst = pairs[2 * pair + 1];
+    if (src < 0 || src >= num_pages || dst < 0 || dst >= num_pages) continue;
+    const uint8_t *from = pages + layer * layer_stride + (int64_t)src * page_bytes;
+    uint8_t *to = pages + layer * layer_stride + (int64_t)dst * page_bytes;
+    const int64_t base = (int64_t)part * kCopyUnitBytes + (int64_t)threadIdx.x * 16;
+    uint4 v[kCopyVecs];
+#pragma unroll
+    for (int32_t k = 0; k < kCopyVecs; ++k) {
+      const int64_t off = base + (int64_t)k * 256 * 16;
+      if (off < page_bytes) v[k] = *reinterpret_cast<const uint4 *>(from + off);
+    }
+#pragma unroll
+    for (int32_t k = 0; k < kCopyVecs; ++k) {
+      const int64_t off = base + (int64_t)k * 256 * 16;
+      if (off < page_bytes) *reinterpret_cast<uint4 *>(to + off) = v[k];
+    }
+  }
+}
 }  // namespace
+
+hipError_t launch_copy_pages(uint8_t *pages, int64_t layer_stride, int32_t layers,
+                             int32_t num_pages, const int32_t *pairs, int32_t n_pairs,
+                             int64_t page_bytes, hipStream_t s) {
+  if (n_pairs <= 0 || layers <= 0) return hipSuccess;
+  const int32_t units_per_page = (int32_t)((page_bytes + kCopyUnitBytes - 1) / kCopyUnitBytes);
+  const int64_t n_units = (int64_t)n_pairs * layers * units_per_page;
+  const unsigned grid = (unsigned)std::min<int64_t>(n_units, 8192);
+  hipLaunchKernelGGL(copy_pages_kernel, dim3(grid), dim3(256), 0, s, pages, layer_stride, layers,
+                     num_pages, pairs, page_bytes, units_per_page, n_units);
+  return hipGetLastError();
+}
 
 hipError_t launch_table_scatter(const int32_t *packed, int32_t n_rows, int32_t W, int32_t n_seqs,
                                 int32_t *tables, int32_t *lens, hipStream_t s) {

@@ -36,6 +36,11 @@ hipError_t launch_f32_to_f16(const float *in, uint16_t *out, int64_t n, int32_t 
 // block-table update: records [seq][W ids] x n_rows, then n_seqs lengths
 hipError_t launch_table_scatter(const int32_t *packed, int32_t n_rows, int32_t W, int32_t n_seqs,
                                 int32_t *tables, int32_t *lens, hipStream_t s);
+// copy-on-write: page dst := page src for each (src, dst) pair in `pairs`
+// (device), in `layers` page arrays `layer_stride` bytes apart
+hipError_t launch_copy_pages(uint8_t *pages, int64_t layer_stride, int32_t layers,
+                             int32_t num_pages, const int32_t *pairs, int32_t n_pairs,
+                             int64_t page_bytes, hipStream_t s);
 
 struct DecodeLaunch {
   Geo g;

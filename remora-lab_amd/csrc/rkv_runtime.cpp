@@ -174,6 +174,15 @@ struct rkv_alloc {
   std::vector<int32_t> lens;       // [max_seqs]
   std::vector<int32_t> held;       // pages held per sequence
   std::vector<uint8_t> dirty;      // table row changed since the last upload (lengths always go)
+  std::vector<int32_t> refs;       // [num_pages] block-table entries naming the page, 0 = free
+  // Copy-on-write copies queued since the last take, as (src, dst) pairs;
+  // copy_src[dst] = src while the pair is queued (else -1) and copy_reads[p]
+  // counts queued pairs that read p.  A page a queued pair reads is never
+  // chosen as a copy destination, so queued copies are independent of each
+  // other and run in any order.
+  std::vector<int32_t> copies;
+  std::vector<int32_t> copy_src;
+  std::vector<int32_t> copy_reads;
 };
 
 namespace {
@@ -185,6 +194,33 @@ rkv_status check_seq(const rkv_alloc *a, int32_t seq, const char *op) {
 }
 int32_t pages_for(const rkv_alloc *a, int64_t len) {
   return (int32_t)((len + a->d.page_tokens - 1) / a->d.page_tokens);
+}
+// Drop one block-table reference to `page`; the last one returns it to the
+// free list and cancels a queued copy into it (nothing reads it any more).
+void release_page(rkv_alloc *a, int32_t page) {
+  if (--a->refs[page] > 0) return;
+  a->free_list.push_back(page);
+  if (a->copy_src[page] < 0) return;
+  --a->copy_reads[a->copy_src[page]];
+  a->copy_src[page] = -1;
+  for (size_t i = 0; i < a->copies.size(); i += 2) {
+    if (a->copies[i + 1] == page) {
+      a->copies.erase(a->copies.begin() + (std::ptrdiff_t)i, a->copies.begin() + (std::ptrdiff_t)i + 2);
+      break;
+    }
+  }
+}
+// Index in the free list of the topmost page no queued copy reads, or -1.
+int32_t copy_target_index(const rkv_alloc *a) {
+  for (int32_t i = (int32_t)a->free_list.size() - 1; i >= 0; --i)
+    if (a->copy_reads[a->free_list[i]] == 0) return i;
+  return -1;
+}
+int32_t take_page(rkv_alloc *a) {
+  const int32_t page = a->free_list.back();
+  a->free_list.pop_back();
+  a->refs[page] = 1;
+  return page;
 }
 }  // namespace
 
@@ -217,6 +253,9 @@ rkv_status rkv_alloc_create(const rkv_alloc_desc *desc, rkv_alloc **out) {
   a->lens.assign(desc->max_seqs, 0);
   a->held.assign(desc->max_seqs, 0);
   a->dirty.assign(desc->max_seqs, 1);
+  a->refs.assign(desc->num_pages, 0);
+  a->copy_src.assign(desc->num_pages, -1);
+  a->copy_reads.assign(desc->num_pages, 0);
   *out = a;
   return RKV_OK;
 }
@@ -236,15 +275,36 @@ rkv_status rkv_seq_reserve(rkv_alloc *a, int32_t seq, int32_t new_len) {
   if (need > a->d.max_pages_per_seq)
     return fail(RKV_ERR_CAPACITY, op, "seq %d: %d tokens need %d pages > max_pages_per_seq %d",
                 seq, new_len, need, a->d.max_pages_per_seq);
-  const int32_t extra = need - a->held[seq];
+  int32_t *row = &a->tables[(size_t)seq * a->d.max_pages_per_seq];
+  const int32_t len = a->lens[seq];
+  // Growing into a partly filled last page that other tables also name:
+  // this sequence gets a private copy of it first (copy-on-write).
+  const int32_t last = len / a->d.page_tokens;
+  const bool cow = new_len > len && len % a->d.page_tokens != 0 && a->refs[row[last]] > 1;
+  const int32_t extra = need - a->held[seq] + (cow ? 1 : 0);
   if (extra > (int32_t)a->free_list.size())
     return fail(RKV_ERR_OUT_OF_PAGES, op, "seq %d needs %d more pages, %zu free", seq, extra,
                 a->free_list.size());
-  int32_t *row = &a->tables[(size_t)seq * a->d.max_pages_per_seq];
-  for (int32_t i = a->held[seq]; i < need; ++i) {
-    row[i] = a->free_list.back();
-    a->free_list.pop_back();
+  if (cow) {
+    const int32_t at = copy_target_index(a);
+    if (at < 0)
+      return fail(RKV_ERR_OUT_OF_PAGES, op,
+                  "seq %d: every free page is still read by a queued copy; sync first", seq);
+    std::swap(a->free_list[at], a->free_list.back());
+    const int32_t shared = row[last];
+    // A queued copy into `shared` has not run yet and no device write can
+    // reach `shared` before it does, so the new copy reads the same source.
+    const int32_t src = a->copy_src[shared] >= 0 ? a->copy_src[shared] : shared;
+    const int32_t page = take_page(a);
+    --a->refs[shared];
+    row[last] = page;
+    a->copies.push_back(src);
+    a->copies.push_back(page);
+    a->copy_src[page] = src;
+    ++a->copy_reads[src];
+    a->dirty[seq] = 1;
   }
+  for (int32_t i = a->held[seq]; i < need; ++i) row[i] = take_page(a);
   if (need > a->held[seq]) a->dirty[seq] = 1;
   a->held[seq] = std::max(a->held[seq], need);
   a->lens[seq] = new_len;
@@ -261,7 +321,7 @@ rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len) {
   int32_t *row = &a->tables[(size_t)seq * a->d.max_pages_per_seq];
   // return pages last-first so a re-grow gets the same pages back
   for (int32_t i = a->held[seq] - 1; i >= keep; --i) {
-    a->free_list.push_back(row[i]);
+    release_page(a, row[i]);
     row[i] = -1;
   }
   if (keep < a->held[seq]) a->dirty[seq] = 1;
@@ -271,6 +331,55 @@ rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len) {
 }
 
 rkv_status rkv_seq_free(rkv_alloc *a, int32_t seq) { return rkv_seq_truncate(a, seq, 0); }
+
+rkv_status rkv_seq_fork(rkv_alloc *a, int32_t src, int32_t dst, int32_t len) {
+  const char *op = "rkv_seq_fork";
+  if (rkv_status s = check_seq(a, src, op)) return s;
+  if (rkv_status s = check_seq(a, dst, op)) return s;
+  if (src == dst) return fail(RKV_ERR_INVALID_ARG, op, "src and dst are both seq %d", src);
+  if (a->held[dst] != 0 || a->lens[dst] != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "dst seq %d is not empty (length %d)", dst, a->lens[dst]);
+  if (len < 0 || len > a->lens[src])
+    return fail(RKV_ERR_INVALID_ARG, op, "len %d outside [0, %d] of seq %d", len, a->lens[src],
+                src);
+  const int32_t n = pages_for(a, len);
+  const int32_t *from = &a->tables[(size_t)src * a->d.max_pages_per_seq];
+  int32_t *to = &a->tables[(size_t)dst * a->d.max_pages_per_seq];
+  for (int32_t i = 0; i < n; ++i) {
+    to[i] = from[i];
+    ++a->refs[from[i]];
+  }
+  a->held[dst] = n;
+  a->lens[dst] = len;
+  a->dirty[dst] = 1;
+  return RKV_OK;
+}
+
+rkv_status rkv_page_refs(const rkv_alloc *a, int32_t page, int32_t *refs) {
+  const char *op = "rkv_page_refs";
+  if (!a || !refs) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  if (page < 0 || page >= a->d.num_pages)
+    return fail(RKV_ERR_INVALID_ARG, op, "page %d outside [0, %d)", page, a->d.num_pages);
+  *refs = a->refs[page];
+  return RKV_OK;
+}
+
+rkv_status rkv_alloc_take_copies(rkv_alloc *a, int32_t *pairs, int32_t cap, int32_t *n) {
+  const char *op = "rkv_alloc_take_copies";
+  if (!a || !n) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  const int32_t count = (int32_t)(a->copies.size() / 2);
+  *n = count;
+  if (count == 0) return RKV_OK;
+  if (!pairs || cap < count)
+    return fail(RKV_ERR_INVALID_ARG, op, "cap %d < %d queued copies", cap, count);
+  std::memcpy(pairs, a->copies.data(), sizeof(int32_t) * a->copies.size());
+  for (int32_t i = 0; i < count; ++i) {
+    a->copy_src[a->copies[2 * i + 1]] = -1;
+    a->copy_reads[a->copies[2 * i]] = 0;
+  }
+  a->copies.clear();
+  return RKV_OK;
+}
 
 rkv_status rkv_seq_len(const rkv_alloc *a, int32_t seq, int32_t *len) {
   const char *op = "rkv_seq_len";
@@ -674,6 +783,25 @@ rkv_status rkv_import_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
   return e == hipSuccess ? RKV_OK : hip_fail(op, e);
 }
 
+rkv_status rkv_copy_pages(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
+                          int64_t layer_stride_bytes, int32_t layers, const int32_t *pairs,
+                          int32_t n_pairs, void *stream) {
+  const char *op = "rkv_copy_pages";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_geometry(g, op)) return s;
+  const int64_t pb = (int64_t)rkv::page_bytes(to_geo(g));
+  if (layers < 1 || n_pairs < 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "layers=%d n_pairs=%d", layers, n_pairs);
+  if (layers > 1 && layer_stride_bytes < pb * g->num_pages)
+    return fail(RKV_ERR_INVALID_ARG, op, "layer stride %lld < %lld bytes of one layer's pages",
+                (long long)layer_stride_bytes, (long long)(pb * g->num_pages));
+  if (n_pairs == 0) return RKV_OK;
+  if (!pages || !pairs) return fail(RKV_ERR_INVALID_ARG, op, "NULL pages or pairs");
+  hipError_t e = rkv::launch_copy_pages(static_cast<uint8_t *>(pages), layer_stride_bytes, layers,
+                                        g->num_pages, pairs, n_pairs, pb, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
 rkv_status rkv_f32_to_f16(rkv_ctx *ctx, const float *in, uint16_t *out, int64_t n, int32_t rule,
                           void *stream) {
   const char *op = "rkv_f32_to_f16";
@@ -803,11 +931,18 @@ struct rkv_pool {
   // table uploads: two pinned host staging buffers (reused every other
   // sync, after the event of their last copy) and one device buffer, all of
   // the packed size max_seqs * (W + 1) + max_seqs int32
+  // ... followed by room for num_pages queued copy-on-write pairs
   int32_t *h_stage[2] = {nullptr, nullptr};
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int32_t *d_stage = nullptr;
   uint32_t n_syncs = 0;
 };
+
+namespace {
+size_t stage_ints(const rkv_pool_desc &d) {
+  return (size_t)d.max_seqs * (d.max_pages_per_seq + 1) + d.max_seqs + 2 * (size_t)d.num_pages;
+}
+}  // namespace
 
 extern "C" {
 
@@ -832,8 +967,7 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
   p->layer_bytes = (size_t)desc->num_pages * rkv::page_bytes(to_geo(&g));
   hipError_t e;
   const size_t tbytes = sizeof(int32_t) * (size_t)desc->max_seqs * desc->max_pages_per_seq;
-  const size_t sbytes =
-      sizeof(int32_t) * ((size_t)desc->max_seqs * (desc->max_pages_per_seq + 1) + desc->max_seqs);
+  const size_t sbytes = sizeof(int32_t) * stage_ints(*desc);
   if ((e = hipMalloc(&p->pages, p->layer_bytes * desc->layers)) != hipSuccess ||
       (e = hipMalloc(&p->d_tables, tbytes)) != hipSuccess ||
       (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess ||
@@ -889,11 +1023,13 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   const char *op = "rkv_pool_sync_tables";
   if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
   if (rkv_status s = use_device(p->ctx, op)) return s;
-  // Stream-ordered upload: the changed rows and every length are packed into
-  // a pinned staging buffer, copied in one transfer and scattered on the
+  // Stream-ordered upload: the changed rows, every length and the queued
+  // copy-on-write pairs are packed into a pinned staging buffer, copied in
+  // one transfer, then the page copies run and the rows are scattered on the
   // device, so launches queued after this call on `stream` see the new
-  // tables and earlier ones the old.  Nothing here waits for the device
-  // unless the staging buffer's copy from two syncs ago is still pending.
+  // tables and copied pages, and earlier ones the old.  Nothing here waits
+  // for the device unless the staging buffer's copy from two syncs ago is
+  // still pending.
   rkv_alloc *a = p->alloc;
   const int32_t W = a->d.max_pages_per_seq;
   const int32_t S = a->d.max_seqs;
@@ -911,12 +1047,19 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
     ++n_rows;
   }
   std::memcpy(h + (size_t)n_rows * (W + 1), a->lens.data(), sizeof(int32_t) * S);
-  const size_t bytes = sizeof(int32_t) * ((size_t)n_rows * (W + 1) + S);
+  const size_t pairs_at = (size_t)n_rows * (W + 1) + S;
+  int32_t n_pairs = 0;
+  if (rkv_status s = rkv_alloc_take_copies(a, h + pairs_at, a->d.num_pages, &n_pairs)) return s;
+  const size_t bytes = sizeof(int32_t) * (pairs_at + 2 * (size_t)n_pairs);
   hipStream_t hs = as_stream(stream);
   if ((e = hipMemcpyAsync(p->d_stage, h, bytes, hipMemcpyHostToDevice, hs)) != hipSuccess)
     return hip_fail(op, e);
   if ((e = hipEventRecord(p->stage_done[slot], hs)) != hipSuccess) return hip_fail(op, e);
   ++p->n_syncs;
+  if ((e = rkv::launch_copy_pages(p->pages, (int64_t)p->layer_bytes, p->d.layers, p->d.num_pages,
+                                  p->d_stage + pairs_at, n_pairs,
+                                  (int64_t)rkv::page_bytes(to_geo(&p->g)), hs)) != hipSuccess)
+    return hip_fail(op, e);
   if ((e = rkv::launch_table_scatter(p->d_stage, n_rows, W, S, p->d_tables, p->d_lens, hs)) !=
       hipSuccess)
     return hip_fail(op, e);
