@@ -189,6 +189,29 @@ typedef struct rkv_decode_args {
                                (per-kernel timing); NULL = none */
 } rkv_decode_args;
 
+/* Chunked prefill attention.  The reference's BatchStepModel::prefill_batch
+ * (har-serve/src/adapter.rs:31-60) folds the one-token step over the chunk,
+ * so query row i of entry e -- at position ctx_lens[e] + i of sequence
+ * seq_ids[e] -- attends positions [0, ctx_lens[e] + i]: exactly the decode
+ * of that length (attention.rs:148-165).  The chunk's own K/V rows must be
+ * appended first (rkv_append_q8 / rkv_pool_append, same stream).  The entry
+ * table is host memory and travels in the kernel arguments. */
+#define RKV_PREFILL_MAX_SEQS 64
+typedef struct rkv_prefill_args {
+  int32_t n_seqs;           /* entries, 0..RKV_PREFILL_MAX_SEQS */
+  const int32_t *seq_ids;   /* host [n_seqs] */
+  const int32_t *ctx_lens;  /* host [n_seqs]: tokens cached before the chunk */
+  const int32_t *q_rows;    /* host [n_seqs]: chunk tokens (query rows), >= 0 */
+  const int32_t *q_offsets; /* host [n_seqs]: the entry's first row in q and out */
+  int32_t total_rows;       /* rows of q and out */
+  const void *q;            /* device [total_rows][q_heads][head_dim], 16-byte aligned */
+  int32_t q_dtype;          /* RKV_F32 | RKV_BF16 */
+  int32_t q_heads;          /* multiple of kv_heads; q_heads/kv_heads divides 128 */
+  float scale;              /* softmax scale on q.k */
+  void *out;                /* device [total_rows][q_heads][head_dim] */
+  int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
+} rkv_prefill_args;
+
 /* ---- kernel-level entry points (explicit device pointers) -----------------
  * pages: one layer's pool (num_pages * rkv_page_bytes).  block_tables:
  * device int32 [n_seqs][bt_stride]; seq_lens: device int32 [n_seqs]. */
@@ -238,6 +261,13 @@ rkv_status rkv_splitk_combine(rkv_ctx *ctx, const float *ml, const float *o,
                               const int32_t *seq_lens, int32_t n_seqs,
                               int32_t partition_tokens, void *out, int32_t out_dtype,
                               void *stream);
+
+/* Chunked prefill attention over the pages (see rkv_prefill_args); rows of
+ * entries whose range exceeds the block-table row (or 4096 pages) are
+ * refused with RKV_ERR_UNSUPPORTED. */
+rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                          const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
+                          const rkv_prefill_args *args, void *stream);
 
 /* Export seq's K or V cache in the reference contiguous layout
  * [kv_heads][len][head_dim/32*34] bytes (what flash_decode_reference reads,
@@ -318,6 +348,10 @@ rkv_status rkv_pool_append(rkv_pool *pool, int32_t layer, const rkv_append_args 
                            void *stream);
 rkv_status rkv_pool_decode(rkv_pool *pool, int32_t layer, const rkv_decode_args *args,
                            void *stream);
+/* rkv_prefill_q8 on a layer; also checks ctx_lens[e] + q_rows[e] against the
+ * allocator's length of each sequence. */
+rkv_status rkv_pool_prefill(rkv_pool *pool, int32_t layer, const rkv_prefill_args *args,
+                            void *stream);
 rkv_status rkv_pool_gather(rkv_pool *pool, int32_t layer, int32_t seq, int32_t kind,
                            uint8_t *out, void *stream);
 

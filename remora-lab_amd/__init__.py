@@ -66,6 +66,15 @@ class DecodeArgs(C.Structure):
                 ("append", C.POINTER(AppendArgs)), ("split_event", P)]
 
 
+class PrefillArgs(C.Structure):
+    _fields_ = [("n_seqs", C.c_int32), ("seq_ids", I32P), ("ctx_lens", I32P), ("q_rows", I32P),
+                ("q_offsets", I32P), ("total_rows", C.c_int32), ("q", P), ("q_dtype", C.c_int32),
+                ("q_heads", C.c_int32), ("scale", C.c_float), ("out", P), ("out_dtype", C.c_int32)]
+
+
+PREFILL_MAX_SEQS = 64
+
+
 class FlashDecodeParams(C.Structure):
     _fields_ = [("q_heads", C.c_int32), ("kv_heads", C.c_int32), ("seq_len", C.c_int32),
                 ("chunk", C.c_int32), ("head_dim", C.c_int32)]
@@ -125,6 +134,9 @@ _SIGS = {
     "rkv_pool_append": (C.c_int32, [P, C.c_int32, C.POINTER(AppendArgs), P]),
     "rkv_pool_decode": (C.c_int32, [P, C.c_int32, C.POINTER(DecodeArgs), P]),
     "rkv_pool_gather": (C.c_int32, [P, C.c_int32, C.c_int32, C.c_int32, P, P]),
+    "rkv_prefill_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32,
+                                   C.POINTER(PrefillArgs), P]),
+    "rkv_pool_prefill": (C.c_int32, [P, C.c_int32, C.POINTER(PrefillArgs), P]),
 }
 
 _lib = None
@@ -330,6 +342,30 @@ def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0
     return a
 
 
+def prefill_args(seq_ids, ctx_lens, q_rows, q, out, scale, q_offsets=None) -> PrefillArgs:
+    """Host entry table (lists of ints) + device q/out [total_rows][q_heads][D].
+    q_offsets defaults to the running sum of q_rows."""
+    import torch
+    n = len(seq_ids)
+    if q_offsets is None:
+        q_offsets, o = [], 0
+        for r in q_rows:
+            q_offsets.append(o)
+            o += int(r)
+    arr = [(C.c_int32 * max(n, 1))(*[int(v) for v in x]) for x in (seq_ids, ctx_lens, q_rows, q_offsets)]
+    a = PrefillArgs(n, *[C.cast(x, I32P) for x in arr], q.shape[0], _ptr(q),
+                    BF16 if q.dtype == torch.bfloat16 else F32, q.shape[1], scale, _ptr(out),
+                    BF16 if out.dtype == torch.bfloat16 else F32)
+    a._refs = (q, out, arr)  # the struct holds raw pointers
+    return a
+
+
+def prefill_q8(ctx: Ctx, g: Geometry, pages, block_tables, n_seqs: int, a: PrefillArgs,
+               stream=None) -> None:
+    check(lib().rkv_prefill_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables),
+                               block_tables.shape[1], n_seqs, C.byref(a), _stream(stream)))
+
+
 def decode_workspace_bytes(g: Geometry, a: DecodeArgs) -> int:
     return lib().rkv_decode_workspace_bytes(C.byref(g), C.byref(a))
 
@@ -433,6 +469,9 @@ class Pool:
 
     def decode(self, layer, a: DecodeArgs, stream=None) -> None:
         check(lib().rkv_pool_decode(self.h, layer, C.byref(a), _stream(stream)))
+
+    def prefill(self, layer, a: PrefillArgs, stream=None) -> None:
+        check(lib().rkv_pool_prefill(self.h, layer, C.byref(a), _stream(stream)))
 
     def gather(self, layer, seq, kind, out, stream=None) -> None:
         check(lib().rkv_pool_gather(self.h, layer, seq, kind, _ptr(out), _stream(stream)))

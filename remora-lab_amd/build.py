@@ -15,7 +15,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "librkv.so")
 OBJDIR = os.path.join(HERE, "_build")
 
-SOURCES = ["rkv_append.hip", "rkv_decode.hip", "rkv_decode_rows32.hip", "rkv_runtime.cpp"]
+SOURCES = ["rkv_append.hip", "rkv_decode.hip", "rkv_decode_rows32.hip", "rkv_prefill.hip",
+           "rkv_runtime.cpp"]
 
 # Per-file extra flags.  rkv_decode.hip: MFMA destinations and accumulators
 # in VGPRs (no AGPR<->VGPR copies around the VALU work on them).  The

@@ -203,12 +203,19 @@ constexpr float kTau = 4.0f;
 __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // One wave's share of the decode of one (partition, batch entry, kv head).
-// With NW = 2 waves per workgroup, wave w owns query rows 16w .. 16w+15 and
-// issues every other copy of each tile; the waves share the LDS stages and
-// meet at two barriers per tile (stage free, tile landed).
-template <int D, int NT, bool kSmall, int NS, int NW = 1>
+// With NW > 1 waves per workgroup, wave w owns query rows 16w .. 16w+15 and
+// issues copy k of each tile when k % NW == w; the waves share the LDS
+// stages and meet at two barriers per tile (stage free, tile landed).
+// kPageList: page ids come from a workgroup list in LDS (any length) instead
+// of one register lane per page (at most 64 pages).
+template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kPageList = false>
 struct Decoder {
   using S = StageShape<D>;
+  static constexpr bool kSplitP = true;    // two-term f16 PV weights (see compute)
+  // With one QK n-tile (at most 8 rows) the PV MFMA's columns 8-15 are free:
+  // they carry the second weight term of rows 0-7 instead of a second MFMA,
+  // and the epilogue adds column c + 8 to column c.
+  static constexpr bool kColSplit = kSplitP && NT == 1;
   static constexpr int NP = (NT + 1) / 2;  // PV n-tiles of 16 rows
   static constexpr int NC = D / 64;        // 64-dim QK steps
   static constexpr int NB = D / 32;        // Q8 blocks per row
@@ -219,6 +226,7 @@ struct Decoder {
   int32_t app_mode;        // 0: no rows to append here; 1: before the first copy; 2: after the prologue copies
   int32_t pg_first;        // first page index (within the sequence) of the partition
   int32_t pidv;            // lane i: page id of the partition's i-th page
+  const __attribute__((address_space(3))) int32_t *pg_lds;  // kPageList: page id of page index i
   const uint8_t *kv_base;  // pages + kv head offset
   uint64_t PB;
   ChunkPlan<D, kSmall> plan;
@@ -238,7 +246,8 @@ struct Decoder {
     const int32_t pi = t0 / g.page_tokens - pg_first;
     using PL = ChunkPlan<D, kSmall>;
     if constexpr (!kSmall) {
-      const int32_t pid = __builtin_amdgcn_readlane(pidv, pi);
+      const int32_t pid = kPageList ? __builtin_amdgcn_readfirstlane(pg_lds[pi])
+                                    : __builtin_amdgcn_readlane(pidv, pi);
       const uint8_t *base = kv_base + (uint64_t)pid * PB;
       const uint32_t s0 = (uint32_t)(t0 % g.page_tokens);
 #pragma unroll
@@ -249,8 +258,11 @@ struct Decoder {
       }
     } else {
       // 16-token pages: the two halves of the tile live in two pages
-      const int32_t pid0 = __builtin_amdgcn_readlane(pidv, pi);
-      const int32_t pid1 = (t0 + 16 < len) ? __builtin_amdgcn_readlane(pidv, pi + 1) : pid0;
+      const int32_t pid0 = kPageList ? __builtin_amdgcn_readfirstlane(pg_lds[pi])
+                                     : __builtin_amdgcn_readlane(pidv, pi);
+      const int32_t pid1 = (t0 + 16 < len) ? (kPageList ? __builtin_amdgcn_readfirstlane(pg_lds[pi + 1])
+                                                        : __builtin_amdgcn_readlane(pidv, pi + 1))
+                                           : pid0;
       const uint8_t *base0 = kv_base + (uint64_t)pid0 * PB;
       const uint8_t *base1 = kv_base + (uint64_t)pid1 * PB;
 #pragma unroll
@@ -336,6 +348,7 @@ struct Decoder {
 
     // ---- online softmax (base 2, lazily rescaled reference max) ----
     uint32_t pp[NP][4];  // p of the lane's 8 tokens as packed f16 pairs
+    uint32_t pl[NP][4];  // kSplitP: p - f16(p), rounded to f16
 #pragma unroll
     for (int np = 0; np < NP; ++np) {
       float s[8];
@@ -353,7 +366,8 @@ struct Decoder {
             if (nt == 2 * np) lo_t = tot;
             else hi_t = tot;
           }
-          const float v = (li < 8 ? lo_t : hi_t) * rmul[np];
+          // kColSplit: lanes li >= 8 hold row li - 8 (the ror-8 sum is symmetric)
+          const float v = (kColSplit || li < 8 ? lo_t : hi_t) * rmul[np];
           const int tok = t0 + 16 * mt + 4 * lg + r;
           const float sv = tok < rlim[np] ? v : -INFINITY;
           s[4 * mt + r] = sv;
@@ -384,11 +398,20 @@ struct Decoder {
       for (int i = 0; i < 4; ++i) {
         const v2h h2 = {(_Float16)pr[2 * i], (_Float16)pr[2 * i + 1]};
         pp[np][i] = __builtin_bit_cast(uint32_t, h2);
+        if constexpr (kSplitP) {
+          const v2h l2 = {(_Float16)(pr[2 * i] - (float)h2[0]), (_Float16)(pr[2 * i + 1] - (float)h2[1])};
+          pl[np][i] = __builtin_bit_cast(uint32_t, l2);
+        }
       }
     }
 
-    // ---- PV: B = p * d_v as packed f16 (one rounding of the exact product of
-    // the f16-rounded p and the stored f16 scale) ----
+    // ---- PV: B = p * d_v as packed f16.  Without kSplitP that is one f16
+    // value per (token, row): p rounded to f16, times the stored f16 scale,
+    // rounded again (up to 2^-11 relative per weight).  With kSplitP a second
+    // operand carries what those roundings drop -- the product's rounding
+    // error, exact from an f16 fma, plus (p - f16(p)) * d_v -- and a second
+    // MFMA on the same V operand adds it, so the weights are exact to about
+    // 2^-22. ----
     // Tokens past the sequence end may carry junk scales; zero them on the
     // last tile so 0 * junk cannot turn into NaN.
     const bool tail = t0 + kTile > len;
@@ -407,14 +430,27 @@ struct Decoder {
       const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
       const uint32_t sc[4] = {(uint32_t)sv[0] & smask[0], (uint32_t)sv[1] & smask[1],
                               (uint32_t)sv[2] & smask[2], (uint32_t)sv[3] & smask[3]};
-      v8h pb[NP];
+      v8h pb[NP], pbl[NP];
 #pragma unroll
       for (int np = 0; np < NP; ++np) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const v2h prod = __builtin_bit_cast(v2h, pp[np][i]) * __builtin_bit_cast(v2h, sc[i]);
-          pb[np][2 * i] = prod[0];
-          pb[np][2 * i + 1] = prod[1];
+          const v2h ph = __builtin_bit_cast(v2h, pp[np][i]);
+          const v2h dv = __builtin_bit_cast(v2h, sc[i]);
+          const v2h prod = ph * dv;
+          v2h hi = prod;
+          if constexpr (kSplitP) {
+            const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
+            const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, err);
+            if constexpr (kColSplit) {
+              if (li >= 8) hi = lo;
+            } else {
+              pbl[np][2 * i] = lo[0];
+              pbl[np][2 * i + 1] = lo[1];
+            }
+          }
+          pb[np][2 * i] = hi[0];
+          pb[np][2 * i + 1] = hi[1];
         }
       }
 #pragma unroll
@@ -428,8 +464,11 @@ struct Decoder {
         i8x4_to_f16(w1, a2, a3);
         const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
 #pragma unroll
-        for (int np = 0; np < NP; ++np)
+        for (int np = 0; np < NP; ++np) {
           oacc[np][2 * blk + hm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[np], oacc[np][2 * blk + hm], 0, 0, 0);
+          if constexpr (kSplitP && !kColSplit)
+            oacc[np][2 * blk + hm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[np], oacc[np][2 * blk + hm], 0, 0, 0);
+        }
       }
     }
   }
@@ -440,6 +479,7 @@ struct Decoder {
   // that many and waits one copy longer for the others.
   __device__ __forceinline__ static void wait_tiles_ahead(int ahead) {
     constexpr int kI = ChunkPlan<D, kSmall>::kInstr / NW;
+    static_assert(kI >= 1, "every wave issues at least one copy per tile");
     if (ahead >= 2) {
       constexpr int n = 2 * kI;
       __builtin_amdgcn_s_waitcnt(kWaitBase | (n & 0xf) | ((n >> 4) << 14));
@@ -497,6 +537,101 @@ struct Decoder {
     }
   }
 };
+
+// One QK n-tile's query operands: lane (n = li, group lg) serves the row
+// whose D values start at element `qbase` of q (qbase < 0: a dead row, all
+// zeros), dims 64*c + 16*lg .. +15.  It is live for the even block (lg < 2)
+// when li < 8 and for the odd block (lg >= 2) when li >= 8.  The row is
+// split into two int8 planes, q ~ sq * (128*hi + lo), and `qmul` returns
+// sq * scale_log2 (the same on every lane of the row).
+template <int D>
+__device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t qbase, int li,
+                                              int lg, float scale_log2, v4i *qhi, v4i *qlo,
+                                              float &qmul) {
+  constexpr int NC = D / 64;
+  float qv[NC][16];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) qv[c][e] = 0.0f;
+  if (qbase >= 0) {
+    const int64_t base = qbase + 16 * lg;
+    if (bf16) {
+      const uint16_t *q = static_cast<const uint16_t *>(qp) + base;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const uint4 w0 = *reinterpret_cast<const uint4 *>(q + 64 * c);
+        const uint4 w1 = *reinterpret_cast<const uint4 *>(q + 64 * c + 8);
+        const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          qv[c][2 * e] = bf16_bits_to_f32((uint16_t)(ws[e] & 0xffffu));
+          qv[c][2 * e + 1] = bf16_bits_to_f32((uint16_t)(ws[e] >> 16));
+        }
+      }
+    } else {
+      const float *q = static_cast<const float *>(qp) + base;
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const float4 w = *reinterpret_cast<const float4 *>(q + 64 * c + 4 * e4);
+          qv[c][4 * e4] = w.x;
+          qv[c][4 * e4 + 1] = w.y;
+          qv[c][4 * e4 + 2] = w.z;
+          qv[c][4 * e4 + 3] = w.w;
+        }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  // q ~ sq * Q with |Q| <= 16256 = 127*128; Q = 128*hi + lo with hi in
+  // [-127, 127] and lo in [-64, 63].
+  const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
+  qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
+  const bool live = (li < 8) == (lg < 2);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    uint32_t hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      int32_t Q = (int32_t)rintf(qv[c][e] * inv);
+      Q = live ? max(-16256, min(16256, Q)) : 0;
+      const int32_t hi = (Q + 64) >> 7;
+      const int32_t lo = Q - 128 * hi;
+      hw[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)hi) << (8 * (e & 3));
+      lw[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)lo) << (8 * (e & 3));
+    }
+    qhi[c] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+    qlo[c] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+  }
+}
+
+// Normalized output row `orow` ([rows][D], f32 or bf16) from one PV n-tile's
+// accumulators: lane (li, lg) holds dims 16*m + 4*lg .. +3 for every m.
+template <int D>
+__device__ __forceinline__ void store_out_row(void *out, bool bf16, int64_t orow, const v4f *oacc,
+                                              float l, int lg) {
+  const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
+#pragma unroll
+  for (int m = 0; m < D / 16; ++m) {
+    const int d0 = 16 * m + 4 * lg;
+    const v4f o = l > 0.0f ? oacc[m] * inv_l : v4f{0.f, 0.f, 0.f, 0.f};
+    if (bf16) {
+      uint16_t *dst = static_cast<uint16_t *>(out) + orow * D + d0;
+      const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(o[0]) | ((uint32_t)f32_to_bf16_rtne(o[1]) << 16);
+      const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(o[2]) | ((uint32_t)f32_to_bf16_rtne(o[3]) << 16);
+      *reinterpret_cast<uint2 *>(dst) = uint2{w0, w1};
+    } else {
+      *reinterpret_cast<v4f *>(static_cast<float *>(out) + orow * D + d0) = o;
+    }
+  }
+}
 #endif  // __HIP_DEVICE_COMPILE__
 
 // Length of batch entry e, 0 when its sequence id or length is out of range
@@ -690,83 +825,27 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   const int32_t R = p.q_len * q_per_kv;
 
   // ---- query: int8 hi/lo planes as MFMA B operands -------------------------
-  // Lane (n = li, group lg) of QK n-tile nt serves row 8*nt + (n & 7), dims
-  // 64*c + 16*lg .. +15; it is live for the even block (lg < 2) when n < 8
-  // and for the odd block (lg >= 2) when n >= 8.
+  // Lane (li, lg) of QK n-tile nt serves row 8*nt + (li & 7) of this wave.
   float qmul[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int row = r0 + 8 * nt + (li & 7);
-    float qv[NC][16];
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) qv[c][e] = 0.0f;
+    int64_t qbase = -1;
     if (row < R) {
       const int j = row / q_per_kv;
       const int h = kvh * q_per_kv + row % q_per_kv;
-      const int64_t base = (((int64_t)b * p.q_len + j) * p.q_heads + h) * D + 16 * lg;
-      if (p.q_bf16) {
-        const uint16_t *q = static_cast<const uint16_t *>(p.q) + base;
-#pragma unroll
-        for (int c = 0; c < NC; ++c) {
-          const uint4 w0 = *reinterpret_cast<const uint4 *>(q + 64 * c);
-          const uint4 w1 = *reinterpret_cast<const uint4 *>(q + 64 * c + 8);
-          const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            qv[c][2 * e] = bf16_bits_to_f32((uint16_t)(ws[e] & 0xffffu));
-            qv[c][2 * e + 1] = bf16_bits_to_f32((uint16_t)(ws[e] >> 16));
-          }
-        }
-      } else {
-        const float *q = static_cast<const float *>(p.q) + base;
-#pragma unroll
-        for (int c = 0; c < NC; ++c)
-#pragma unroll
-          for (int e4 = 0; e4 < 4; ++e4) {
-            const float4 w = *reinterpret_cast<const float4 *>(q + 64 * c + 4 * e4);
-            qv[c][4 * e4] = w.x;
-            qv[c][4 * e4 + 1] = w.y;
-            qv[c][4 * e4 + 2] = w.z;
-            qv[c][4 * e4 + 3] = w.w;
-          }
-      }
+      qbase = (((int64_t)b * p.q_len + j) * p.q_heads + h) * D;
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
-    amax = fmaxf(amax, __shfl_xor(amax, 16));
-    amax = fmaxf(amax, __shfl_xor(amax, 32));
-    // q ~ sq * Q with |Q| <= 16256 = 127*128; Q = 128*hi + lo with hi in
-    // [-127, 127] and lo in [-64, 63].
-    const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
-    qmul[nt] = amax > 0.0f ? (amax / 16256.0f) * p.scale_log2 : 0.0f;
-    const bool live = (li < 8) == (lg < 2);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      uint32_t hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        int32_t Q = (int32_t)rintf(qv[c][e] * inv);
-        Q = live ? max(-16256, min(16256, Q)) : 0;
-        const int32_t hi = (Q + 64) >> 7;
-        const int32_t lo = Q - 128 * hi;
-        hw[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)hi) << (8 * (e & 3));
-        lw[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)lo) << (8 * (e & 3));
-      }
-      dc.qhi[nt][c] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
-      dc.qlo[nt][c] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
-    }
+    load_q_planes<D>(p.q, p.q_bf16 != 0, qbase, li, lg, p.scale_log2, dc.qhi[nt], dc.qlo[nt],
+                     qmul[nt]);
   }
 
   // ---- per-lane softmax rows: PV n-tile np, column li -> row 16*np + li ---
 #pragma unroll
   for (int np = 0; np < NP; ++np) {
-    const int row = r0 + 16 * np + li;
-    const int nt = 2 * np + (li >> 3);
+    // kColSplit: lanes li and li + 8 both follow row li & 7
+    const int row = r0 + 16 * np + (Dec::kColSplit ? (li & 7) : li);
+    const int nt = Dec::kColSplit ? 0 : 2 * np + (li >> 3);
     // every lane of column li computed the scale of row 8*nt + (li & 7)
     float mul = 0.0f;
 #pragma unroll
@@ -800,31 +879,25 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
 
   // ---- epilogue ---------------------------------------------------------------
+  if constexpr (Dec::kColSplit) {
+    // column li + 8 holds the second weight term of row li
+#pragma unroll
+    for (int m = 0; m < D / 16; ++m)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dc.oacc[0][m][r] += dpp_ror8(dc.oacc[0][m][r]);
+  }
 #pragma unroll
   for (int np = 0; np < NP; ++np) {
     float l = dc.lrun[np];
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     const int row = r0 + 16 * np + li;
-    if (row >= R) continue;
+    if (row >= R || (Dec::kColSplit && li >= 8)) continue;
     const int j = row / q_per_kv;
     const int h = kvh * q_per_kv + row % q_per_kv;
     const int64_t orow = ((int64_t)b * p.q_len + j) * p.q_heads + h;
     if (p.ws_o == nullptr) {
-      const float inv_l = l > 0.0f ? 1.0f / l : 0.0f;
-#pragma unroll
-      for (int m = 0; m < D / 16; ++m) {
-        const int d0 = 16 * m + 4 * lg;
-        const v4f o = l > 0.0f ? dc.oacc[np][m] * inv_l : v4f{0.f, 0.f, 0.f, 0.f};
-        if (p.out_bf16) {
-          uint16_t *dst = static_cast<uint16_t *>(p.out) + orow * D + d0;
-          const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(o[0]) | ((uint32_t)f32_to_bf16_rtne(o[1]) << 16);
-          const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(o[2]) | ((uint32_t)f32_to_bf16_rtne(o[3]) << 16);
-          *reinterpret_cast<uint2 *>(dst) = uint2{w0, w1};
-        } else {
-          *reinterpret_cast<v4f *>(static_cast<float *>(p.out) + orow * D + d0) = o;
-        }
-      }
+      store_out_row<D>(p.out, p.out_bf16 != 0, orow, dc.oacc[np], l, lg);
     } else {
       const int64_t prow = p.ws_hdr != nullptr
                                ? ((int64_t)kvh * p.n_wg + (int64_t)blockIdx.x) * R + row

@@ -91,6 +91,28 @@ struct DecodeLaunch {
 };
 // rows per kv head = q_len * q_heads / kv_heads must be <= 32
 hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s);
+
+// Chunked prefill attention: entry e holds rows[e] query rows of sequence
+// seq[e] at positions ctx[e] .. ctx[e]+rows[e]-1 (already appended), stored
+// at rows qoff[e].. of q/out ([rows][q_heads][head_dim]); row i attends
+// positions [0, ctx[e]+i].  Workgroup x of the grid (first[n_entries],
+// kv_heads) takes row block x - first[e] of the entry with first[e] <= x <
+// first[e+1]: tq query tokens x q_heads/kv_heads heads = kPrefillRows rows.
+constexpr int kPrefillWaves = 8;
+constexpr int kPrefillRows = 16 * kPrefillWaves;
+constexpr int kPrefillMaxEntries = 64;
+constexpr int kPrefillMaxPages = 4096;  // page-list capacity of one row block (LDS)
+struct PrefillLaunch {
+  DecodeLaunch d;  // geometry, pages, tables, q, out, dtypes, scale, fault, stages
+  int32_t tq;
+  int32_t n_entries;
+  int32_t seq[kPrefillMaxEntries];
+  int32_t ctx[kPrefillMaxEntries];
+  int32_t rows[kPrefillMaxEntries];
+  int32_t qoff[kPrefillMaxEntries];
+  int32_t first[kPrefillMaxEntries + 1];
+};
+hipError_t launch_prefill(const PrefillLaunch &pf, hipStream_t s);
 // the 17..32-row instantiations (own translation unit)
 hipError_t launch_decode_rows32(const DecodeLaunch &d, hipStream_t s);
 

@@ -619,9 +619,90 @@ rkv_status check_tables(const void *pages, const int32_t *bt, int32_t bt_stride,
   return RKV_OK;
 }
 
+// Arguments of a prefill call, and the launch's entry table (row blocks of
+// kPrefillRows rows per kv head, in entry order).
+rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                        const int32_t *bt, int32_t bt_stride, int32_t n_seqs,
+                        const rkv_prefill_args *a, const char *op, rkv::PrefillLaunch &pf) {
+  if (rkv_status s = check_geometry(g, op)) return s;
+  if (rkv_status s = check_tables(pages, bt, bt_stride, n_seqs, op)) return s;
+  if (!a) return fail(RKV_ERR_INVALID_ARG, op, "args is NULL");
+  if (a->n_seqs < 0 || a->n_seqs > RKV_PREFILL_MAX_SEQS)
+    return fail(RKV_ERR_INVALID_ARG, op, "n_seqs=%d outside [0, %d]", a->n_seqs,
+                RKV_PREFILL_MAX_SEQS);
+  if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "q_heads=%d is not a multiple of kv_heads=%d",
+                a->q_heads, g->kv_heads);
+  const int32_t G = a->q_heads / g->kv_heads;
+  if (rkv::kPrefillRows % G != 0)
+    return fail(RKV_ERR_UNSUPPORTED, op, "q_heads/kv_heads=%d does not divide %d", G,
+                rkv::kPrefillRows);
+  if (a->q_dtype != RKV_F32 && a->q_dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, op, "q_dtype=%d", a->q_dtype);
+  if (a->out_dtype != RKV_F32 && a->out_dtype != RKV_BF16)
+    return fail(RKV_ERR_UNSUPPORTED, op, "out_dtype=%d", a->out_dtype);
+  if (!(std::isfinite(a->scale))) return fail(RKV_ERR_INVALID_ARG, op, "scale is not finite");
+  if (a->total_rows < 0) return fail(RKV_ERR_INVALID_ARG, op, "total_rows=%d", a->total_rows);
+  if (a->n_seqs > 0 && (!a->seq_ids || !a->ctx_lens || !a->q_rows || !a->q_offsets))
+    return fail(RKV_ERR_INVALID_ARG, op, "NULL seq_ids/ctx_lens/q_rows/q_offsets");
+  pf = rkv::PrefillLaunch{};
+  pf.tq = rkv::kPrefillRows / G;
+  pf.n_entries = a->n_seqs;
+  int64_t blocks = 0;
+  for (int32_t e = 0; e < a->n_seqs; ++e) {
+    const int32_t seq = a->seq_ids[e], c = a->ctx_lens[e], n = a->q_rows[e], off = a->q_offsets[e];
+    if (seq < 0 || seq >= n_seqs)
+      return fail(RKV_ERR_INVALID_ARG, op, "entry %d: seq %d outside [0, %d)", e, seq, n_seqs);
+    if (c < 0 || n < 0 || off < 0 || (int64_t)off + n > a->total_rows)
+      return fail(RKV_ERR_INVALID_ARG, op, "entry %d: ctx_len=%d q_rows=%d q_offset=%d total_rows=%d",
+                  e, c, n, off, a->total_rows);
+    const int64_t end = (int64_t)c + n;
+    if (end > (int64_t)bt_stride * g->page_tokens ||
+        (end + g->page_tokens - 1) / g->page_tokens > rkv::kPrefillMaxPages)
+      return fail(RKV_ERR_UNSUPPORTED, op, "entry %d: %lld tokens exceed the table row (%d pages, "
+                  "at most %d)", e, (long long)end, bt_stride, rkv::kPrefillMaxPages);
+    pf.seq[e] = seq;
+    pf.ctx[e] = c;
+    pf.rows[e] = n;
+    pf.qoff[e] = off;
+    pf.first[e] = (int32_t)blocks;
+    blocks += (n + pf.tq - 1) / pf.tq;
+  }
+  pf.first[a->n_seqs] = (int32_t)blocks;
+  if (blocks > 0 && (!a->q || !a->out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL q/out");
+  if (blocks > (int64_t)1 << 30) return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
+  rkv::DecodeLaunch &d = pf.d;
+  d.g = to_geo(g);
+  d.pages = static_cast<const uint8_t *>(pages);
+  d.bt = bt;
+  d.bt_stride = bt_stride;
+  d.n_seqs = n_seqs;
+  d.q = a->q;
+  d.q_bf16 = a->q_dtype == RKV_BF16;
+  d.q_heads = a->q_heads;
+  d.scale_log2 = a->scale * 1.4426950408889634f;
+  d.out = a->out;
+  d.out_bf16 = a->out_dtype == RKV_BF16;
+  d.fault = ctx->d_fault;
+  d.stages = 2;
+  return RKV_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                          const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
+                          const rkv_prefill_args *a, void *stream) {
+  const char *op = "rkv_prefill_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  rkv::PrefillLaunch pf;
+  if (rkv_status s = make_prefill(ctx, g, pages, block_tables, bt_stride, n_seqs, a, op, pf))
+    return s;
+  hipError_t e = rkv::launch_prefill(pf, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
 
 rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
                          const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
@@ -1087,6 +1168,24 @@ rkv_status rkv_pool_decode(rkv_pool *p, int32_t layer, const rkv_decode_args *ar
   if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
   return rkv_decode_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
                        p->d.max_pages_per_seq, p->d_lens, p->d.max_seqs, args, stream);
+}
+
+rkv_status rkv_pool_prefill(rkv_pool *p, int32_t layer, const rkv_prefill_args *args,
+                            void *stream) {
+  const char *op = "rkv_pool_prefill";
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
+  if (args) {
+    for (int32_t e = 0; e < args->n_seqs && args->seq_ids && args->ctx_lens && args->q_rows; ++e) {
+      const int32_t seq = args->seq_ids[e];
+      if (seq < 0 || seq >= p->d.max_seqs) continue;  // reported by the kernel-level check
+      if ((int64_t)args->ctx_lens[e] + args->q_rows[e] > p->alloc->lens[seq])
+        return fail(RKV_ERR_INVALID_ARG, op, "entry %d: ctx_len %d + q_rows %d > length %d of seq %d",
+                    e, args->ctx_lens[e], args->q_rows[e], p->alloc->lens[seq], seq);
+    }
+  }
+  return rkv_prefill_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
+                        p->d.max_pages_per_seq, p->d.max_seqs, args, stream);
 }
 
 rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind, uint8_t *out,

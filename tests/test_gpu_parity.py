@@ -256,6 +256,9 @@ def test_config1_decode(rkv, rko, ctx):
     (8, 4, 256, 64, [1024, 999], False, False),
     (4, 4, 128, 16, [517, 64, 1], False, True),
     (32, 2, 128, 128, [3000], True, False),
+    # a few tokens each: the outlier channels (|v| up to ~30) are averaged
+    # over almost nothing, so every weight's rounding shows
+    (16, 2, 256, 64, [2, 3, 5, 9, 17, 40], True, False),
 ])
 def test_decode_parity(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_bf16, out_bf16):
     print(f"decode Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens}", flush=True)

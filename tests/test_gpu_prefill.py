@@ -1,0 +1,192 @@
+"""Chunked prefill attention on the GPU against the oracle, through the C ABI.
+
+The reference's prefill (BatchStepModel::prefill_batch, adapter.rs:31-60)
+folds the one-token step over the chunk, so row i of a chunk after ctx
+cached tokens must equal flash_decode_reference over the first ctx+i+1 rows
+(attention.rs:148-165).  The oracle's paged decode with q_len = chunk rows
+and length ctx+chunk computes exactly that per row (row j attends
+len - q_len + j + 1 positions).  Bars as in test_gpu_parity.py: max-abs
+2e-3 and relative 1e-3 over each entry's output."""
+import numpy as np
+import pytest
+
+from tests.test_gpu_parity import ATOL, RTOL, Scene, _as_u8, _bind_ctx, assert_close  # noqa: F401
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def _oracle(rko, sc, seq, ctx, n, q, scale):
+    lens = np.array(sc.lens, np.int32).copy()
+    lens[seq] = ctx + n
+    return rko.paged_decode(sc.lay, sc.pages, sc.bt, lens, np.array([seq], np.int32),
+                            q[None], scale, 1024)[0]
+
+
+def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, seed=0):
+    """entries: (seq, ctx, n) with ctx + n <= the sequence's length."""
+    torch = _torch()
+    rng = np.random.default_rng(seed)
+    D = sc.D
+    rows = [n for _, _, n in entries]
+    total = max(sum(rows), 1)
+    q = rng.standard_normal((total, Hq, D)).astype(np.float32)
+    if q_bf16:
+        q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    qd = torch.from_numpy(q).cuda()
+    if q_bf16:
+        qd = qd.to(torch.bfloat16)
+    out = torch.full((total, Hq, D), float("nan"), device="cuda",
+                     dtype=torch.bfloat16 if out_bf16 else torch.float32)
+    a = rkv.prefill_args([s for s, _, _ in entries], [c for _, c, _ in entries], rows, qd, out, scale)
+    rkv.prefill_q8(ctx_h, sc.g, sc.pages_d, sc.bt_d, len(sc.lens), a)
+    ctx_h.sync()
+    got = out.float().cpu().numpy()
+    off = 0
+    for s, c, n in entries:
+        if n:
+            want = _oracle(rko, sc, s, c, n, q[off:off + n], scale)
+            g = got[off:off + n]
+            if out_bf16:
+                # the f32 result rounded once to bf16 (half an ulp = 2^-9 relative)
+                assert float((np.abs(g - want) - np.abs(want) * 2.0 ** -8).max()) <= ATOL
+                assert np.linalg.norm(g - want) / np.linalg.norm(want) <= RTOL + 2.0 ** -8
+            else:
+                assert_close(g, want, what=f"seq {s} ctx {c} rows {n}")
+        off += n
+    return got
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,PT,entries,q_bf16,out_bf16,outliers", [
+    # G = 8 (16 chunk tokens per row block): chunk from empty, mid-page, a
+    # block-sized chunk, one row, a long context
+    (16, 2, 256, 64, [(0, 40), (300, 17), (129, 128), (64, 1), (1000, 70)], True, False, 0.01),
+    # config 1 geometry (G = 4, 16-token pages: half-tile pages)
+    (8, 2, 128, 16, [(0, 33), (200, 100), (31, 2)], False, False, 0.0),
+    (8, 2, 128, 32, [(5, 64), (77, 45)], False, True, 0.0),
+    # G = 1 (128 tokens per block) and G = 16 (8 tokens per block)
+    (16, 16, 128, 64, [(10, 150), (0, 7)], True, False, 0.0),
+    (32, 2, 128, 128, [(250, 23), (0, 9)], True, False, 0.01),
+])
+def test_prefill_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16, out_bf16, outliers):
+    lens = [c + n + extra for (c, n), extra in zip(entries, [3, 0, 5, 0, 2])]
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=len(entries) + D, outliers=outliers,
+               src_bf16=q_bf16)
+    ent = [(i, c, n) for i, (c, n) in enumerate(entries)]
+    _run(rkv, rko, ctx, sc, ent, Hq, 1.0 / np.sqrt(D), q_bf16, out_bf16, seed=D + PT)
+
+
+def test_prefill_entries_share_a_sequence(rkv, rko, ctx):
+    """Two entries of one call read the same sequence at different chunk
+    boundaries, entries with zero rows are skipped, and q_offsets may leave
+    gaps: rows outside every entry stay untouched."""
+    torch = _torch()
+    Hq, Hkv, D, PT = 16, 2, 256, 64
+    sc = Scene(rkv, rko, Hkv, D, PT, [500, 90], seed=3)
+    rng = np.random.default_rng(4)
+    total = 120
+    q = rng.standard_normal((total, Hq, D)).astype(np.float32)
+    qd = torch.from_numpy(q).cuda()
+    out = torch.full((total, Hq, D), 7.0, device="cuda")
+    ent = [(0, 100, 30), (1, 0, 0), (0, 400, 50), (1, 60, 30)]
+    offs = [0, 30, 35, 90]
+    a = rkv.prefill_args([e[0] for e in ent], [e[1] for e in ent], [e[2] for e in ent], qd, out,
+                         0.0625, q_offsets=offs)
+    rkv.prefill_q8(ctx, sc.g, sc.pages_d, sc.bt_d, 2, a)
+    ctx.sync()
+    got = out.cpu().numpy()
+    for (s, c, n), o in zip(ent, offs):
+        if n:
+            want = _oracle(rko, sc, s, c, n, q[o:o + n], 0.0625)
+            assert_close(got[o:o + n], want, what=f"seq {s} ctx {c}")
+    assert np.all(got[30:35] == 7.0) and np.all(got[85:90] == 7.0)
+
+
+def test_prefill_rejects_bad_arguments(rkv, rko, ctx):
+    torch = _torch()
+    Hkv, D, PT = 2, 128, 16
+    sc = Scene(rkv, rko, Hkv, D, PT, [40], seed=5)
+    q = torch.zeros((8, 8, D), device="cuda")
+    out = torch.zeros_like(q)
+
+    def call(seq_ids, ctxs, rows, qq=q, oo=out, offs=None):
+        a = rkv.prefill_args(seq_ids, ctxs, rows, qq, oo, 1.0, q_offsets=offs)
+        rkv.prefill_q8(ctx, sc.g, sc.pages_d, sc.bt_d, 1, a)
+
+    cases = [
+        (([1], [0], [4]), rkv.ERR_INVALID_ARG),            # seq outside the table
+        (([0], [-1], [4]), rkv.ERR_INVALID_ARG),           # negative ctx
+        (([0], [0], [9]), rkv.ERR_INVALID_ARG),            # rows beyond q/out
+        (([0], [41], [8]), rkv.ERR_UNSUPPORTED),           # beyond the table row (48 tokens)
+    ]
+    for args, status in cases:
+        with pytest.raises(rkv.RkvError) as e:
+            call(*args)
+        assert e.value.status == status, (args, e.value)
+    with pytest.raises(rkv.RkvError) as e:
+        call([0], [0], [4], offs=[6])                      # offset + rows > total rows
+    assert e.value.status == rkv.ERR_INVALID_ARG
+    q12 = torch.zeros((8, 24, D), device="cuda")           # 12 q heads per kv head
+    with pytest.raises(rkv.RkvError) as e:
+        call([0], [0], [4], qq=q12, oo=torch.zeros_like(q12))
+    assert e.value.status == rkv.ERR_UNSUPPORTED
+    many = rkv.PREFILL_MAX_SEQS + 1
+    with pytest.raises(rkv.RkvError) as e:
+        call([0] * many, [0] * many, [0] * many)
+    assert e.value.status == rkv.ERR_INVALID_ARG
+    ctx.sync()
+
+
+def test_pool_chunked_prefill_then_decode(rkv, rko, ctx):
+    """A 300-token prompt through the pool in chunks of 128, 128 and 44
+    (reserve, sync, append, prefill per chunk), on two layers; every chunk's
+    rows equal the oracle, and the prompt's last row equals the pool decode
+    of the same query at length 300."""
+    torch = _torch()
+    Hkv, D, PT, Hq, layers = 2, 256, 64, 16, 2
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, 32, 2, 8, seed=7)
+    rng = np.random.default_rng(8)
+    prompt = rng.standard_normal((300, Hkv, D)).astype(np.float32)
+    q = rng.standard_normal((300, Hq, D)).astype(np.float32)
+    outs = {layer: np.zeros((300, Hq, D), np.float32) for layer in range(layers)}
+    done = 0
+    for n in (128, 128, 44):
+        pool.alloc.reserve(0, done + n)
+        pool.sync_tables()
+        for layer in range(layers):
+            kd = torch.from_numpy(prompt[done:done + n] * (layer + 1)).cuda()
+            pool.append(layer, torch.zeros(n, dtype=torch.int32, device="cuda"),
+                        torch.arange(done, done + n, dtype=torch.int32, device="cuda"), kd, kd)
+            qd = torch.from_numpy(q[done:done + n]).cuda()
+            out = torch.empty_like(qd)
+            pool.prefill(layer, rkv.prefill_args([0], [done], [n], qd, out, 0.0625))
+            ctx.sync()
+            outs[layer][done:done + n] = out.cpu().numpy()
+        done += n
+    with pytest.raises(rkv.RkvError):
+        pool.prefill(0, rkv.prefill_args([0], [250], [51], torch.zeros((51, Hq, D), device="cuda"),
+                                         torch.zeros((51, Hq, D), device="cuda"), 1.0))
+    tables, lens = pool.alloc.export()
+    lay = rko.layout(Hkv, D, PT, 32)
+    pb = rkv.page_bytes(pool.geometry)
+    for layer in range(layers):
+        pages = _as_u8(pool.layer_pages(layer), 32 * pb).cpu().numpy()
+        want = rko.paged_decode(lay, pages, tables, lens, np.array([0], np.int32), q[None],
+                                0.0625, 1024)[0]
+        assert_close(outs[layer], want, what=f"layer {layer} prompt")
+    # the last prompt row through the decode kernel
+    qd = torch.from_numpy(q[299:300][None]).cuda()
+    o = torch.empty_like(qd)
+    sid = torch.zeros(1, dtype=torch.int32, device="cuda")
+    a = rkv.decode_args(qd, o, sid, 0.0625, 8 * PT)
+    ws = torch.zeros(max(rkv.decode_workspace_bytes(pool.geometry, a), 4), dtype=torch.uint8,
+                     device="cuda")
+    a = rkv.decode_args(qd, o, sid, 0.0625, 8 * PT, workspace=ws)
+    pool.decode(layers - 1, a)
+    ctx.sync()
+    assert_close(o.cpu().numpy()[0, 0], outs[layers - 1][299], what="decode vs prefill row")
+    pool.close()
