@@ -61,7 +61,8 @@ def parse():
     ap.add_argument("--partition-tokens", type=int, default=0)
     ap.add_argument("--config", type=int, default=1,
                     help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs; "
-                         "6 = prefix-shared decode (forks + copy-on-write pages)")
+                         "6 = prefix-shared decode (forks + copy-on-write pages); "
+                         "7 = chunked prefill attention")
     ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
     ap.add_argument("--append-launch", action="store_true",
                     help="append the step's rows with a separate rkv_pool_append launch instead "
@@ -753,8 +754,88 @@ def run_config6(args) -> int:
     return 0
 
 
+def run_config7(args) -> int:
+    """Chunked prefill: 8 sequences, each with ctx=8192 cached tokens and a
+    512-row chunk (config 4's prefill rows, at its median context).  One step
+    and layer appends the chunk's K/V rows (rkv_pool_append) and runs the
+    prefill attention over them (rkv_pool_prefill), rotating over 4 layer
+    pools.  Rows of a chunk attend causally: row i sees ctx + i + 1 tokens.
+    `value` is attention TFLOP/s, 4*D flops per (query row, visible token),
+    against the dense f16 MFMA peak; the prefill kernel is HIP-event timed."""
+    import numpy as np
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    Hq, Hkv, D, PT = 16, 2, 256, 64
+    B, layers, C0, N = 8, 4, 8192, 512
+    L = C0 + N
+    pps = (L + PT - 1) // PT
+    num_pages = int(math.ceil(B * pps * 1.10))
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, num_pages, B, pps, seed=args.seed)
+    for s in range(B):
+        pool.alloc.reserve(s, L)
+    pool.sync_tables()
+    for layer in range(layers):
+        _fill_layer(rkv, pool, layer, range(B), [L] * B, Hkv, D, args.seed)
+    ctx.sync()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 5)
+    rows = B * N
+    sid = torch.arange(B, device=dev, dtype=torch.int32).repeat_interleave(N)
+    pos = (torch.arange(N, device=dev, dtype=torch.int32) + C0).repeat(B)
+    k_new = torch.randn((rows, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    v_new = torch.randn((rows, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    q = torch.randn((rows, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    out = torch.empty((rows, Hq, D), device=dev, dtype=torch.float32)
+    pa = rkv.prefill_args(list(range(B)), [C0] * B, [N] * B, q, out, 1.0 / math.sqrt(D))
+    stream = torch.cuda.current_stream()
+
+    def step(i, ev):
+        layer = i % layers
+        pool.append(layer, sid, pos, k_new, v_new, stream=stream)
+        if ev is not None:
+            ev[0].record(stream)
+        pool.prefill(layer, pa, stream=stream)
+        if ev is not None:
+            ev[1].record(stream)
+
+    wall, kern = _time_steps(args, stream, step)
+    ctx.sync()
+    row_tokens = B * sum(C0 + i + 1 for i in range(N))
+    flops = 4 * D * Hq * row_tokens
+    kv_bytes = B * L * Hkv * 2 * (D // 32 * 34)
+    peak = 2500.0
+    res = {
+        "metric": "config 7: chunked prefill attention TFLOP/s (dense f16 MFMA peak 2.5 PFLOP/s)",
+        "value": round(flops / wall / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 QK (two q planes) + f16 PV (two-term weights), f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
+        "config": {"workload": (f"chunked prefill: B={B} sequences, ctx={C0} cached + {N}-row chunk "
+                                f"each (causal), Hq=16, Hkv=2, D=256, page 64, append + attention "
+                                f"per step, {layers} rotating layer pools"),
+                   "batch": B, "ctx": C0, "chunk_rows": N, "layers_rotated": layers},
+        "us_per_step": round(wall * 1e6, 2),
+        "flops_per_step": flops,
+        "roofline": {"bound": "mfma", "kernel": "rkv::prefill_kernel<256, false, 2>",
+                     "achieved": round(flops / kern / 1e12, 2), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(flops / kern / 1e12 / peak, 4), "traffic": None,
+                     "prefill_us": round(kern * 1e6, 2)},
+        "kv_bytes_per_layer": kv_bytes,
+    }
+    print(json.dumps(res), flush=True)
+    pool.close()
+    ctx.close()
+    return 0
+
+
 if __name__ == "__main__":
     _a = parse()
+    if _a.config == 7:
+        sys.exit(run_config7(_a))
     if _a.config == 4:
         sys.exit(run_config4(_a))
     if _a.config == 6:
