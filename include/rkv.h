@@ -48,7 +48,10 @@ enum {
   RKV_ERR_BAD_BLOCK_TABLE = -3,/* page id / position outside the pool */
   RKV_ERR_UNSUPPORTED = -4,    /* head_dim, page size or dtype not built */
   RKV_ERR_DEVICE = -5,         /* HIP runtime error (HarError.result) */
-  RKV_ERR_CAPACITY = -6        /* sequence longer than its block-table row */
+  RKV_ERR_CAPACITY = -6,       /* sequence longer than its block-table row */
+  RKV_ERR_REFUSED = -7         /* R4KV page refused by a fail-closed check
+                                  (r4kv/src/page.rs RestoreError); the reason
+                                  is an rkv_r4kv_refusal code */
 };
 
 enum { RKV_F32 = 0, RKV_BF16 = 1 };                 /* element types */
@@ -354,6 +357,110 @@ rkv_status rkv_pool_prefill(rkv_pool *pool, int32_t layer, const rkv_prefill_arg
                             void *stream);
 rkv_status rkv_pool_gather(rkv_pool *pool, int32_t layer, int32_t seq, int32_t kind,
                            uint8_t *out, void *stream);
+
+/* ---- R4KV pages: off-HBM tier spill / restore ------------------------------
+ * The container of har/crates/r4kv/src/page.rs: a 96-byte little-endian
+ * header with a trailing CRC32C of its first 92 bytes (PageHeader::to_bytes,
+ * :100-126), then the payload body and a CRC32C of the body (pack_page,
+ * :213-224).  CRC32C is crc32c.rs:1-31 (reflected 0x82f63b78, init and
+ * final xor 0xffffffff).  Restores fail closed (check_restore, :151-210). */
+#define RKV_R4KV_HEADER_BYTES 96
+#define RKV_R4KV_MAGIC 0x52344B56u /* "R4KV", page.rs:11 */
+#define RKV_R4KV_VERSION 1
+enum { RKV_FMT_F16 = 0, RKV_FMT_Q8 = 1, RKV_FMT_Q6 = 2, RKV_FMT_Q4 = 3, RKV_FMT_Q3 = 4 }; /* lib.rs:23-31 */
+typedef struct rkv_r4kv_header {  /* PageHeader, page.rs:15-30 */
+  uint64_t prefix_digest;
+  uint32_t token_start;
+  uint32_t token_count;
+  uint32_t pos_start;
+  uint16_t layer_lo;
+  uint16_t layer_hi;   /* inclusive */
+  uint8_t k_fmt;
+  uint8_t v_fmt;
+  uint32_t epoch;
+  uint32_t generation;
+  uint64_t payload_len; /* body bytes, without the trailing CRC */
+  uint32_t sketch_offset;
+  uint16_t flags;       /* bit0 has_sketch, bit1 rotated_k */
+} rkv_r4kv_header;
+/* RestoreError variants (page.rs:63-76) */
+enum {
+  RKV_R4KV_ACCEPTED = 0,
+  RKV_R4KV_BAD_MAGIC = 1,
+  RKV_R4KV_BAD_VERSION = 2,
+  RKV_R4KV_HEADER_CHECKSUM = 3,
+  RKV_R4KV_PAYLOAD_CHECKSUM = 4,
+  RKV_R4KV_LENGTH = 5,
+  RKV_R4KV_PREFIX = 6,
+  RKV_R4KV_TOKEN_RANGE = 7,
+  RKV_R4KV_POS = 8,
+  RKV_R4KV_LAYER_RANGE = 9,
+  RKV_R4KV_FORMAT = 10,
+  RKV_R4KV_GENERATION = 11
+};
+/* RestoreExpectation (page.rs:32-45); k_fmt / v_fmt < 0 = any; the
+ * generation predicate is generation_min <= generation <= generation_max
+ * when check_generation is non-zero. */
+typedef struct rkv_r4kv_expect {
+  uint64_t prefix_digest;
+  uint32_t token_start;
+  uint32_t pos_start;
+  uint16_t layer_lo;
+  uint16_t layer_hi;
+  int32_t k_fmt;
+  int32_t v_fmt;
+  int32_t check_generation;
+  uint32_t generation_min;
+  uint32_t generation_max;
+} rkv_r4kv_expect;
+
+/* Host CRC32C (crc32c.rs:23-31). */
+uint32_t rkv_crc32c_host(const uint8_t *data, size_t n);
+/* CRC32C of n device bytes (16-byte aligned) into *out (device word),
+ * stream-ordered.  No reference counterpart on the device: crc32c.rs is
+ * CPU-only. */
+rkv_status rkv_crc32c(rkv_ctx *ctx, const void *data, uint64_t n, uint32_t *out, void *stream);
+/* PageHeader::to_bytes / from_bytes (page.rs:100-149).  decode sets
+ * *refusal (BAD_MAGIC, BAD_VERSION, HEADER_CHECKSUM, FORMAT) and returns
+ * RKV_ERR_REFUSED when the bytes are refused. */
+rkv_status rkv_r4kv_header_encode(const rkv_r4kv_header *h, uint8_t out[RKV_R4KV_HEADER_BYTES]);
+rkv_status rkv_r4kv_header_decode(const uint8_t in[RKV_R4KV_HEADER_BYTES], rkv_r4kv_header *h,
+                                  int32_t *refusal);
+/* PageHeader::check_restore (page.rs:151-210), same order of checks. */
+rkv_status rkv_r4kv_check_restore(const rkv_r4kv_header *h, const rkv_r4kv_expect *e,
+                                  uint64_t payload_body_len, int32_t *refusal);
+/* unpack_page (page.rs:227-260) on host bytes: header, body length and the
+ * payload CRC.  On success *body points into `page`. */
+rkv_status rkv_r4kv_unpack_host(const uint8_t *page, size_t len, rkv_r4kv_header *h,
+                                const uint8_t **body, int32_t *refusal);
+
+/* Page size of a spill: 96 + layers*2*kv_heads*token_count*(head_dim/32*34) + 4. */
+size_t rkv_r4kv_page_bytes(const rkv_pool *pool, int32_t token_count, int32_t layer_lo,
+                           int32_t layer_hi);
+/* Spill (the T1 mirror of r4kv/src/tier.rs): rows of tokens [token_start,
+ * token_start+token_count) of `seq`, layers [layer_lo, layer_hi], become one
+ * R4KV page: header from `identity` (prefix_digest, pos_start, epoch,
+ * generation, flags bit1; the rest is set here: k_fmt = v_fmt = Q8,
+ * payload_len, no sketch), body = per layer, K then V, per kv head, the
+ * reference rows (attention.rs:144-147 layout), then the body's CRC32C
+ * computed on the device.  The page is assembled in `staging` (device,
+ * >= rkv_r4kv_page_bytes) and then copied to `dst` (host or device, may be
+ * `staging` itself), all ordered on `stream`. */
+rkv_status rkv_pool_spill(rkv_pool *pool, int32_t seq, int32_t token_start, int32_t token_count,
+                          int32_t layer_lo, int32_t layer_hi, const rkv_r4kv_header *identity,
+                          void *staging, size_t staging_bytes, void *dst, size_t dst_bytes,
+                          void *stream);
+/* Restore (promotion): `page` (host bytes) is unpacked and gated on the
+ * host -- header, length, identity against `expect` -- before any device
+ * work; its body is copied to `staging` (device, >= the page size) and its
+ * CRC32C checked on the device (the call waits for that one word); only
+ * then are the rows written into the pages of `seq`, at the header's token
+ * range (which must lie within the sequence's reserved length), for the
+ * header's layers.  A refused page returns RKV_ERR_REFUSED with *refusal
+ * set and writes nothing. */
+rkv_status rkv_pool_restore(rkv_pool *pool, int32_t seq, const uint8_t *page, size_t page_bytes,
+                            const rkv_r4kv_expect *expect, void *staging, size_t staging_bytes,
+                            int32_t *refusal, void *stream);
 
 #ifdef __cplusplus
 }

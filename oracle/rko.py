@@ -58,8 +58,19 @@ class GroupStats(C.Structure):
 P = C.c_void_p
 
 
+class R4kvHeader(C.Structure):
+    _fields_ = [("prefix_digest", C.c_uint64), ("token_start", C.c_uint32),
+                ("token_count", C.c_uint32), ("pos_start", C.c_uint32), ("layer_lo", C.c_uint16),
+                ("layer_hi", C.c_uint16), ("k_fmt", C.c_uint8), ("v_fmt", C.c_uint8),
+                ("epoch", C.c_uint32), ("generation", C.c_uint32), ("payload_len", C.c_uint64),
+                ("sketch_offset", C.c_uint32), ("flags", C.c_uint16)]
+
+
 def _declare(L):
     sig = {
+        "rko_crc32c": (C.c_uint32, [P, C.c_size_t]),
+        "rko_r4kv_header_bytes": (None, [P, P]),
+        "rko_r4kv_pack_page": (None, [P, P, C.c_size_t, P]),
         "rko_splitmix64": (C.c_uint64, [C.c_uint64]),
         "rko_seeded_float": (C.c_float, [C.c_uint64]),
         "rko_lcg_values": (None, [P, C.c_size_t, C.c_uint64]),
@@ -317,3 +328,28 @@ def paged_decode(L: Layout, pages, block_tables, seq_lens, seq_ids, q: np.ndarra
     if rc != 0:
         raise ValueError(f"oracle paged_decode failed rc={rc}")
     return out
+
+
+def crc32c(data) -> int:
+    b = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else \
+        np.ascontiguousarray(data, np.uint8).reshape(-1)
+    return int(lib().rko_crc32c(_p(b) if b.size else None, b.size))
+
+
+def r4kv_header(**fields) -> R4kvHeader:
+    return R4kvHeader(**fields)
+
+
+def r4kv_header_bytes(h: R4kvHeader) -> bytes:
+    out = np.zeros(96, np.uint8)
+    lib().rko_r4kv_header_bytes(C.byref(h), _p(out))
+    return out.tobytes()
+
+
+def r4kv_pack_page(h: R4kvHeader, body) -> bytes:
+    b = np.ascontiguousarray(np.frombuffer(bytes(body), np.uint8) if not isinstance(body, np.ndarray)
+                             else body, np.uint8).reshape(-1)
+    out = np.zeros(96 + b.size + 4, np.uint8)
+    lib().rko_r4kv_pack_page(C.byref(h), _p(b) if b.size else None, b.size, _p(out))
+    return out.tobytes()
+

@@ -708,3 +708,57 @@ int32_t rko_paged_decode(const rko_layout *L, const uint8_t *pages,
   free(o);
   return 0;
 }
+
+/* ---- R4KV page container ----------------------------------------------------- */
+
+/* har/crates/r4kv/src/crc32c.rs:4-21 (table) and :23-31 (loop) */
+uint32_t rko_crc32c(const uint8_t *data, size_t n) {
+  static uint32_t table[256];
+  static int ready = 0;
+  if (!ready) {
+    for (uint32_t i = 0; i < 256; ++i) {
+      uint32_t c = i;
+      for (int k = 0; k < 8; ++k) c = (c & 1u) ? (0x82f63b78u ^ (c >> 1)) : (c >> 1);
+      table[i] = c;
+    }
+    ready = 1;
+  }
+  uint32_t c = 0xffffffffu;
+  for (size_t i = 0; i < n; ++i) c = table[(c ^ data[i]) & 0xffu] ^ (c >> 8);
+  return c ^ 0xffffffffu;
+}
+
+/* page.rs:78-86 put_u16/put_u32/put_u64 (little endian) */
+static void le_put(uint8_t *b, size_t off, uint64_t v, int bytes) {
+  for (int i = 0; i < bytes; ++i) b[off + (size_t)i] = (uint8_t)(v >> (8 * i));
+}
+
+/* page.rs:100-126 */
+void rko_r4kv_header_bytes(const rko_r4kv_header *h, uint8_t out[96]) {
+  memset(out, 0, 96);
+  le_put(out, 0, 0x52344B56u, 4); /* MAGIC "R4KV", page.rs:11 */
+  le_put(out, 4, 1, 2);           /* VERSION, page.rs:12 */
+  le_put(out, 6, h->flags, 2);
+  le_put(out, 8, h->prefix_digest, 8);
+  le_put(out, 16, h->token_start, 4);
+  le_put(out, 20, h->token_count, 4);
+  le_put(out, 24, h->pos_start, 4);
+  le_put(out, 28, h->layer_lo, 2);
+  le_put(out, 30, h->layer_hi, 2);
+  out[32] = h->k_fmt;
+  out[33] = h->v_fmt;
+  le_put(out, 34, h->epoch, 4);
+  le_put(out, 38, h->generation, 4);
+  le_put(out, 42, h->payload_len, 8);
+  le_put(out, 50, h->sketch_offset, 4);
+  /* 54..92 reserved zeros */
+  le_put(out, 92, rko_crc32c(out, 92), 4);
+}
+
+/* page.rs:213-224 */
+void rko_r4kv_pack_page(const rko_r4kv_header *h, const uint8_t *body, size_t n, uint8_t *out) {
+  rko_r4kv_header_bytes(h, out);
+  if (n) memcpy(out + 96, body, n);
+  le_put(out, 96 + n, rko_crc32c(body, n), 4);
+}
+

@@ -162,6 +162,26 @@ int32_t rko_paged_decode(const rko_layout *L, const uint8_t *pages,
                          int32_t q_len, int32_t q_heads, const float *q, float scale,
                          int32_t chunk, float *out);
 
+/* ---- R4KV page container ---------------------------------------------------- */
+/* har/crates/r4kv/src/crc32c.rs:4-31: reflected 0x82f63b78, init/final xor ~0 */
+uint32_t rko_crc32c(const uint8_t *data, size_t n);
+/* har/crates/r4kv/src/page.rs:15-30 */
+typedef struct rko_r4kv_header {
+  uint64_t prefix_digest;
+  uint32_t token_start, token_count, pos_start;
+  uint16_t layer_lo, layer_hi;
+  uint8_t k_fmt, v_fmt;
+  uint32_t epoch, generation;
+  uint64_t payload_len;
+  uint32_t sketch_offset;
+  uint16_t flags;
+} rko_r4kv_header;
+/* PageHeader::to_bytes, page.rs:100-126 */
+void rko_r4kv_header_bytes(const rko_r4kv_header *h, uint8_t out[96]);
+/* pack_page, page.rs:213-224: header, body, LE CRC32C of the body;
+ * `out` holds 96 + n + 4 bytes */
+void rko_r4kv_pack_page(const rko_r4kv_header *h, const uint8_t *body, size_t n, uint8_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,13 +23,20 @@ ERR_BAD_BLOCK_TABLE = -3
 ERR_UNSUPPORTED = -4
 ERR_DEVICE = -5
 ERR_CAPACITY = -6
+ERR_REFUSED = -7
 
 F32, BF16 = 0, 1
 Q8_CANONICAL, Q8_HARSERVE = 0, 1
 K, V = 0, 1
 
 _STATUS_NAMES = {0: "OK", -1: "INVALID_ARG", -2: "OUT_OF_PAGES", -3: "BAD_BLOCK_TABLE",
-                 -4: "UNSUPPORTED", -5: "DEVICE", -6: "CAPACITY"}
+                 -4: "UNSUPPORTED", -5: "DEVICE", -6: "CAPACITY", -7: "REFUSED"}
+
+# R4KV refusal reasons (RestoreError, r4kv/src/page.rs:63-76) and formats
+R4KV_ACCEPTED, R4KV_BAD_MAGIC, R4KV_BAD_VERSION, R4KV_HEADER_CHECKSUM = 0, 1, 2, 3
+R4KV_PAYLOAD_CHECKSUM, R4KV_LENGTH, R4KV_PREFIX, R4KV_TOKEN_RANGE = 4, 5, 6, 7
+R4KV_POS, R4KV_LAYER_RANGE, R4KV_FORMAT, R4KV_GENERATION = 8, 9, 10, 11
+FMT_F16, FMT_Q8, FMT_Q6, FMT_Q4, FMT_Q3 = 0, 1, 2, 3, 4
 
 
 class RkvError(RuntimeError):
@@ -73,6 +80,21 @@ class PrefillArgs(C.Structure):
 
 
 PREFILL_MAX_SEQS = 64
+
+
+class R4kvHeader(C.Structure):
+    _fields_ = [("prefix_digest", C.c_uint64), ("token_start", C.c_uint32),
+                ("token_count", C.c_uint32), ("pos_start", C.c_uint32), ("layer_lo", C.c_uint16),
+                ("layer_hi", C.c_uint16), ("k_fmt", C.c_uint8), ("v_fmt", C.c_uint8),
+                ("epoch", C.c_uint32), ("generation", C.c_uint32), ("payload_len", C.c_uint64),
+                ("sketch_offset", C.c_uint32), ("flags", C.c_uint16)]
+
+
+class R4kvExpect(C.Structure):
+    _fields_ = [("prefix_digest", C.c_uint64), ("token_start", C.c_uint32),
+                ("pos_start", C.c_uint32), ("layer_lo", C.c_uint16), ("layer_hi", C.c_uint16),
+                ("k_fmt", C.c_int32), ("v_fmt", C.c_int32), ("check_generation", C.c_int32),
+                ("generation_min", C.c_uint32), ("generation_max", C.c_uint32)]
 
 
 class FlashDecodeParams(C.Structure):
@@ -137,6 +159,19 @@ _SIGS = {
     "rkv_prefill_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32,
                                    C.POINTER(PrefillArgs), P]),
     "rkv_pool_prefill": (C.c_int32, [P, C.c_int32, C.POINTER(PrefillArgs), P]),
+    "rkv_crc32c_host": (C.c_uint32, [P, C.c_size_t]),
+    "rkv_crc32c": (C.c_int32, [P, P, C.c_uint64, P, P]),
+    "rkv_r4kv_header_encode": (C.c_int32, [C.POINTER(R4kvHeader), P]),
+    "rkv_r4kv_header_decode": (C.c_int32, [P, C.POINTER(R4kvHeader), I32P]),
+    "rkv_r4kv_check_restore": (C.c_int32, [C.POINTER(R4kvHeader), C.POINTER(R4kvExpect),
+                                           C.c_uint64, I32P]),
+    "rkv_r4kv_unpack_host": (C.c_int32, [P, C.c_size_t, C.POINTER(R4kvHeader),
+                                         C.POINTER(P), I32P]),
+    "rkv_r4kv_page_bytes": (C.c_size_t, [P, C.c_int32, C.c_int32, C.c_int32]),
+    "rkv_pool_spill": (C.c_int32, [P, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                   C.POINTER(R4kvHeader), P, C.c_size_t, P, C.c_size_t, P]),
+    "rkv_pool_restore": (C.c_int32, [P, C.c_int32, P, C.c_size_t, C.POINTER(R4kvExpect), P,
+                                     C.c_size_t, I32P, P]),
 }
 
 _lib = None
@@ -366,6 +401,67 @@ def prefill_q8(ctx: Ctx, g: Geometry, pages, block_tables, n_seqs: int, a: Prefi
                                block_tables.shape[1], n_seqs, C.byref(a), _stream(stream)))
 
 
+def _host_buf(data):
+    import numpy as np
+    b = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8) if not hasattr(data, "dtype")
+                             else data, np.uint8).reshape(-1)
+    return b, (b.ctypes.data_as(P) if b.size else None)
+
+
+def crc32c_host(data) -> int:
+    b, ptr = _host_buf(data)
+    return int(lib().rkv_crc32c_host(ptr, b.size))
+
+
+def crc32c(ctx: Ctx, data, n: int, out, stream=None) -> None:
+    """CRC32C of n bytes of a device tensor into the int32 device tensor `out`."""
+    check(lib().rkv_crc32c(ctx.h, _ptr(data), n, _ptr(out), _stream(stream)))
+
+
+class R4kvRefused(RkvError):
+    def __init__(self, status, message, refusal):
+        super().__init__(status, message)
+        self.refusal = refusal
+
+
+def _check_refusal(status: int, refusal) -> None:
+    if status == ERR_REFUSED:
+        raise R4kvRefused(status, lib().rkv_last_error().decode(), refusal.value)
+    check(status)
+
+
+def r4kv_header_encode(h: R4kvHeader) -> bytes:
+    import numpy as np
+    out = np.zeros(96, np.uint8)
+    check(lib().rkv_r4kv_header_encode(C.byref(h), out.ctypes.data_as(P)))
+    return out.tobytes()
+
+
+def r4kv_header_decode(data) -> R4kvHeader:
+    b, ptr = _host_buf(data)
+    h = R4kvHeader()
+    why = C.c_int32()
+    _check_refusal(lib().rkv_r4kv_header_decode(ptr, C.byref(h), C.byref(why)), why)
+    return h
+
+
+def r4kv_check_restore(h: R4kvHeader, e: R4kvExpect, payload_body_len: int) -> None:
+    why = C.c_int32()
+    _check_refusal(lib().rkv_r4kv_check_restore(C.byref(h), C.byref(e), payload_body_len,
+                                                C.byref(why)), why)
+
+
+def r4kv_unpack_host(page):
+    """(header, body bytes) of a page held in host memory; raises R4kvRefused."""
+    b, ptr = _host_buf(page)
+    h = R4kvHeader()
+    body = P()
+    why = C.c_int32()
+    _check_refusal(lib().rkv_r4kv_unpack_host(ptr, b.size, C.byref(h), C.byref(body),
+                                              C.byref(why)), why)
+    return h, bytes(b[96:96 + h.payload_len])
+
+
 def decode_workspace_bytes(g: Geometry, a: DecodeArgs) -> int:
     return lib().rkv_decode_workspace_bytes(C.byref(g), C.byref(a))
 
@@ -472,6 +568,31 @@ class Pool:
 
     def prefill(self, layer, a: PrefillArgs, stream=None) -> None:
         check(lib().rkv_pool_prefill(self.h, layer, C.byref(a), _stream(stream)))
+
+    def r4kv_page_bytes(self, token_count, layer_lo, layer_hi) -> int:
+        return lib().rkv_r4kv_page_bytes(self.h, token_count, layer_lo, layer_hi)
+
+    def spill(self, seq, token_start, token_count, layer_lo, layer_hi, identity: R4kvHeader,
+              staging, dst, stream=None) -> None:
+        """R4KV page of the range into `staging` (device tensor), copied to
+        `dst` (a host or device tensor, or staging itself)."""
+        check(lib().rkv_pool_spill(self.h, seq, token_start, token_count, layer_lo, layer_hi,
+                                   C.byref(identity), _ptr(staging),
+                                   staging.numel() * staging.element_size(), _ptr(dst),
+                                   dst.numel() * dst.element_size(), _stream(stream)))
+
+    def restore(self, seq, page, expect: R4kvExpect, staging, stream=None) -> None:
+        """Restore a page held in host memory (bytes / numpy / CPU tensor);
+        raises R4kvRefused with .refusal set when a fail-closed check fails."""
+        import numpy as np
+        if hasattr(page, "numpy"):
+            page = page.numpy()
+        b, ptr = _host_buf(page)
+        why = C.c_int32()
+        st = lib().rkv_pool_restore(self.h, seq, ptr, b.size, C.byref(expect), _ptr(staging),
+                                    staging.numel() * staging.element_size(), C.byref(why),
+                                    _stream(stream))
+        _check_refusal(st, why)
 
     def gather(self, layer, seq, kind, out, stream=None) -> None:
         check(lib().rkv_pool_gather(self.h, layer, seq, kind, _ptr(out), _stream(stream)))

@@ -113,6 +113,26 @@ struct PrefillLaunch {
   int32_t first[kPrefillMaxEntries + 1];
 };
 hipError_t launch_prefill(const PrefillLaunch &pf, hipStream_t s);
+
+// CRC32C of n bytes at `data` (16-byte aligned, device-readable) into *out
+// (device word), stream-ordered; the word is cleared by the launch itself.
+hipError_t launch_crc32c(const uint8_t *data, int64_t n, uint32_t *out, hipStream_t s);
+
+// R4KV page body <-> pool: rows of tokens [t0, t0+count) of one sequence
+// (block-table row `bt`), layers [layer_lo, layer_lo+n_layers) of page
+// arrays layer_stride bytes apart.  Pack writes header, body and payload
+// CRC (through crc_word) to page_out; unpack writes a verified body back.
+struct R4kvLaunch {
+  Geo g;
+  int64_t layer_stride;
+  int32_t layer_lo, n_layers;
+  int32_t t0, count;
+  uint8_t header[96];
+};
+hipError_t launch_r4kv_pack(const R4kvLaunch &r, const uint8_t *pages, const int32_t *bt,
+                            uint8_t *page_out, uint32_t *crc_word, int32_t *fault, hipStream_t s);
+hipError_t launch_r4kv_unpack(const R4kvLaunch &r, uint8_t *pages, const int32_t *bt,
+                              const uint8_t *body, int32_t *fault, hipStream_t s);
 // the 17..32-row instantiations (own translation unit)
 hipError_t launch_decode_rows32(const DecodeLaunch &d, hipStream_t s);
 

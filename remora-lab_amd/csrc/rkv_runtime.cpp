@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "../../include/rkv.h"
+#include "rkv_crc32c.h"
 #include "rkv_launch.h"
 
 using rkv::Geo;
@@ -1017,6 +1018,9 @@ struct rkv_pool {
   hipEvent_t stage_done[2] = {nullptr, nullptr};
   int32_t *d_stage = nullptr;
   uint32_t n_syncs = 0;
+  // R4KV page CRC: device result word and its pinned host copy
+  uint32_t *d_crc = nullptr;
+  uint32_t *h_crc = nullptr;
 };
 
 namespace {
@@ -1056,7 +1060,9 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
       (e = hipHostMalloc(&p->h_stage[0], sbytes, hipHostMallocDefault)) != hipSuccess ||
       (e = hipHostMalloc(&p->h_stage[1], sbytes, hipHostMallocDefault)) != hipSuccess ||
       (e = hipEventCreateWithFlags(&p->stage_done[0], hipEventDisableTiming)) != hipSuccess ||
-      (e = hipEventCreateWithFlags(&p->stage_done[1], hipEventDisableTiming)) != hipSuccess) {
+      (e = hipEventCreateWithFlags(&p->stage_done[1], hipEventDisableTiming)) != hipSuccess ||
+      (e = hipMalloc(&p->d_crc, 256)) != hipSuccess ||
+      (e = hipHostMalloc(&p->h_crc, 256, hipHostMallocDefault)) != hipSuccess) {
     rkv_status s = fail(RKV_ERR_DEVICE, op, "allocating %zu page bytes and tables: %s",
                         p->layer_bytes * desc->layers, hipGetErrorString(e));
     rkv_pool_destroy(p);
@@ -1089,6 +1095,8 @@ rkv_status rkv_pool_destroy(rkv_pool *p) {
   (void)hipFree(p->d_tables);
   (void)hipFree(p->d_lens);
   (void)hipFree(p->d_stage);
+  (void)hipFree(p->d_crc);
+  if (p->h_crc) (void)hipHostFree(p->h_crc);
   for (int i = 0; i < 2; ++i) {
     if (p->h_stage[i]) (void)hipHostFree(p->h_stage[i]);
     if (p->stage_done[i]) (void)hipEventDestroy(p->stage_done[i]);
@@ -1197,6 +1205,279 @@ rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind
   return rkv_gather_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer),
                        p->d_tables + (size_t)seq * p->d.max_pages_per_seq, p->alloc->lens[seq],
                        kind, out, stream);
+}
+
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// R4KV pages (r4kv/src/page.rs)
+// ---------------------------------------------------------------------------
+namespace {
+
+void put16(uint8_t *b, int off, uint16_t v) {
+  for (int i = 0; i < 2; ++i) b[off + i] = (uint8_t)(v >> (8 * i));
+}
+void put32(uint8_t *b, int off, uint32_t v) {
+  for (int i = 0; i < 4; ++i) b[off + i] = (uint8_t)(v >> (8 * i));
+}
+void put64(uint8_t *b, int off, uint64_t v) {
+  for (int i = 0; i < 8; ++i) b[off + i] = (uint8_t)(v >> (8 * i));
+}
+uint16_t get16(const uint8_t *b, int off) { return (uint16_t)(b[off] | (b[off + 1] << 8)); }
+uint32_t get32(const uint8_t *b, int off) {
+  uint32_t v = 0;
+  for (int i = 0; i < 4; ++i) v |= (uint32_t)b[off + i] << (8 * i);
+  return v;
+}
+uint64_t get64(const uint8_t *b, int off) {
+  uint64_t v = 0;
+  for (int i = 0; i < 8; ++i) v |= (uint64_t)b[off + i] << (8 * i);
+  return v;
+}
+
+const char *refusal_name(int32_t r) {
+  static const char *names[] = {"accepted", "BadMagic", "BadVersion", "HeaderChecksumMismatch",
+                                "PayloadChecksumMismatch", "LengthMismatch", "PrefixMismatch",
+                                "TokenRangeMismatch", "PosMismatch", "LayerRangeInsufficient",
+                                "FormatRefused", "GenerationRejected"};
+  return r >= 0 && r <= RKV_R4KV_GENERATION ? names[r] : "unknown";
+}
+
+rkv_status refuse(int32_t *refusal, int32_t why, const char *op, const char *detail) {
+  if (refusal) *refusal = why;
+  return fail(RKV_ERR_REFUSED, op, "%s (%s)", refusal_name(why), detail);
+}
+
+size_t spill_body_bytes(const rkv_pool *p, int64_t count, int32_t n_layers) {
+  return (size_t)n_layers * 2 * (size_t)p->d.kv_heads * (size_t)count * rkv_row_bytes(p->d.head_dim);
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t rkv_crc32c_host(const uint8_t *data, size_t n) {
+  return data || n == 0 ? rkv::crc::crc32c(data, n) : 0u;
+}
+
+rkv_status rkv_crc32c(rkv_ctx *ctx, const void *data, uint64_t n, uint32_t *out, void *stream) {
+  const char *op = "rkv_crc32c";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (!out || (n > 0 && !data)) return fail(RKV_ERR_INVALID_ARG, op, "NULL data/out");
+  if (reinterpret_cast<uintptr_t>(data) % 16 != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "data is not 16-byte aligned");
+  if (n >= ((uint64_t)1 << rkv::crc::kShiftBits))
+    return fail(RKV_ERR_UNSUPPORTED, op, "n=%llu bytes (< 2^40)", (unsigned long long)n);
+  hipError_t e = rkv::launch_crc32c(static_cast<const uint8_t *>(data), (int64_t)n, out,
+                                    as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+rkv_status rkv_r4kv_header_encode(const rkv_r4kv_header *h, uint8_t out[RKV_R4KV_HEADER_BYTES]) {
+  if (!h || !out) return fail(RKV_ERR_INVALID_ARG, "rkv_r4kv_header_encode", "NULL argument");
+  std::memset(out, 0, RKV_R4KV_HEADER_BYTES);
+  put32(out, 0, RKV_R4KV_MAGIC);
+  put16(out, 4, RKV_R4KV_VERSION);
+  put16(out, 6, h->flags);
+  put64(out, 8, h->prefix_digest);
+  put32(out, 16, h->token_start);
+  put32(out, 20, h->token_count);
+  put32(out, 24, h->pos_start);
+  put16(out, 28, h->layer_lo);
+  put16(out, 30, h->layer_hi);
+  out[32] = h->k_fmt;
+  out[33] = h->v_fmt;
+  put32(out, 34, h->epoch);
+  put32(out, 38, h->generation);
+  put64(out, 42, h->payload_len);
+  put32(out, 50, h->sketch_offset);
+  put32(out, 92, rkv::crc::crc32c(out, 92));  // 54..92 reserved zeros
+  return RKV_OK;
+}
+
+rkv_status rkv_r4kv_header_decode(const uint8_t in[RKV_R4KV_HEADER_BYTES], rkv_r4kv_header *h,
+                                  int32_t *refusal) {
+  const char *op = "rkv_r4kv_header_decode";
+  if (refusal) *refusal = RKV_R4KV_ACCEPTED;
+  if (!in || !h) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  if (get32(in, 0) != RKV_R4KV_MAGIC) return refuse(refusal, RKV_R4KV_BAD_MAGIC, op, "magic");
+  if (get16(in, 4) != RKV_R4KV_VERSION) return refuse(refusal, RKV_R4KV_BAD_VERSION, op, "version");
+  if (rkv::crc::crc32c(in, 92) != get32(in, 92))
+    return refuse(refusal, RKV_R4KV_HEADER_CHECKSUM, op, "header CRC32C");
+  if (in[32] > RKV_FMT_Q3) return refuse(refusal, RKV_R4KV_FORMAT, op, "k_fmt");
+  if (in[33] > RKV_FMT_Q3) return refuse(refusal, RKV_R4KV_FORMAT, op, "v_fmt");
+  h->flags = get16(in, 6);
+  h->prefix_digest = get64(in, 8);
+  h->token_start = get32(in, 16);
+  h->token_count = get32(in, 20);
+  h->pos_start = get32(in, 24);
+  h->layer_lo = get16(in, 28);
+  h->layer_hi = get16(in, 30);
+  h->k_fmt = in[32];
+  h->v_fmt = in[33];
+  h->epoch = get32(in, 34);
+  h->generation = get32(in, 38);
+  h->payload_len = get64(in, 42);
+  h->sketch_offset = get32(in, 50);
+  return RKV_OK;
+}
+
+rkv_status rkv_r4kv_check_restore(const rkv_r4kv_header *h, const rkv_r4kv_expect *e,
+                                  uint64_t payload_body_len, int32_t *refusal) {
+  const char *op = "rkv_r4kv_check_restore";
+  if (refusal) *refusal = RKV_R4KV_ACCEPTED;
+  if (!h || !e) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  char msg[128];
+  if (payload_body_len != h->payload_len) {
+    std::snprintf(msg, sizeof msg, "declared %llu, actual %llu", (unsigned long long)h->payload_len,
+                  (unsigned long long)payload_body_len);
+    return refuse(refusal, RKV_R4KV_LENGTH, op, msg);
+  }
+  if (h->prefix_digest != e->prefix_digest) {
+    std::snprintf(msg, sizeof msg, "want %016llx, got %016llx", (unsigned long long)e->prefix_digest,
+                  (unsigned long long)h->prefix_digest);
+    return refuse(refusal, RKV_R4KV_PREFIX, op, msg);
+  }
+  if (h->token_start != e->token_start) {
+    std::snprintf(msg, sizeof msg, "want %u, got %u", e->token_start, h->token_start);
+    return refuse(refusal, RKV_R4KV_TOKEN_RANGE, op, msg);
+  }
+  if (h->pos_start != e->pos_start) {
+    std::snprintf(msg, sizeof msg, "want %u, got %u", e->pos_start, h->pos_start);
+    return refuse(refusal, RKV_R4KV_POS, op, msg);
+  }
+  if (h->layer_lo > e->layer_lo || h->layer_hi < e->layer_hi) {
+    std::snprintf(msg, sizeof msg, "want [%u, %u], got [%u, %u]", e->layer_lo, e->layer_hi,
+                  h->layer_lo, h->layer_hi);
+    return refuse(refusal, RKV_R4KV_LAYER_RANGE, op, msg);
+  }
+  if (e->k_fmt >= 0 && e->k_fmt != h->k_fmt) return refuse(refusal, RKV_R4KV_FORMAT, op, "k_fmt");
+  if (e->v_fmt >= 0 && e->v_fmt != h->v_fmt) return refuse(refusal, RKV_R4KV_FORMAT, op, "v_fmt");
+  if (e->check_generation && (h->generation < e->generation_min || h->generation > e->generation_max))
+    return refuse(refusal, RKV_R4KV_GENERATION, op, "generation predicate");
+  return RKV_OK;
+}
+
+rkv_status rkv_r4kv_unpack_host(const uint8_t *page, size_t len, rkv_r4kv_header *h,
+                                const uint8_t **body, int32_t *refusal) {
+  const char *op = "rkv_r4kv_unpack_host";
+  if (refusal) *refusal = RKV_R4KV_ACCEPTED;
+  if (!h || (len > 0 && !page)) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  if (len < RKV_R4KV_HEADER_BYTES + 4) return refuse(refusal, RKV_R4KV_LENGTH, op, "shorter than 100 bytes");
+  if (rkv_status s = rkv_r4kv_header_decode(page, h, refusal)) return s;
+  const size_t body_len = len - RKV_R4KV_HEADER_BYTES - 4;
+  if (body_len != h->payload_len) return refuse(refusal, RKV_R4KV_LENGTH, op, "body length");
+  const uint8_t *b = page + RKV_R4KV_HEADER_BYTES;
+  if (rkv::crc::crc32c(b, body_len) != get32(b, (int)body_len))
+    return refuse(refusal, RKV_R4KV_PAYLOAD_CHECKSUM, op, "payload CRC32C");
+  if (body) *body = b;
+  return RKV_OK;
+}
+
+size_t rkv_r4kv_page_bytes(const rkv_pool *p, int32_t token_count, int32_t layer_lo,
+                           int32_t layer_hi) {
+  if (!p || token_count < 0 || layer_lo < 0 || layer_hi < layer_lo || layer_hi >= p->d.layers)
+    return 0;
+  return RKV_R4KV_HEADER_BYTES + spill_body_bytes(p, token_count, layer_hi - layer_lo + 1) + 4;
+}
+
+rkv_status rkv_pool_spill(rkv_pool *p, int32_t seq, int32_t token_start, int32_t token_count,
+                          int32_t layer_lo, int32_t layer_hi, const rkv_r4kv_header *identity,
+                          void *staging, size_t staging_bytes, void *dst, size_t dst_bytes,
+                          void *stream) {
+  const char *op = "rkv_pool_spill";
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  if (rkv_status s = check_seq(p->alloc, seq, op)) return s;
+  if (!identity) return fail(RKV_ERR_INVALID_ARG, op, "identity is NULL");
+  if (token_start < 0 || token_count < 0 ||
+      (int64_t)token_start + token_count > p->alloc->lens[seq])
+    return fail(RKV_ERR_INVALID_ARG, op, "tokens [%d, +%d) outside the %d of seq %d", token_start,
+                token_count, p->alloc->lens[seq], seq);
+  const size_t need = rkv_r4kv_page_bytes(p, token_count, layer_lo, layer_hi);
+  if (need == 0) return fail(RKV_ERR_INVALID_ARG, op, "layers [%d, %d] of %d", layer_lo, layer_hi, p->d.layers);
+  if (!staging || staging_bytes < need || !dst || dst_bytes < need)
+    return fail(RKV_ERR_INVALID_ARG, op, "staging %zu / dst %zu bytes < %zu", staging_bytes,
+                dst_bytes, need);
+  if (reinterpret_cast<uintptr_t>(staging) % 16 != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "staging is not 16-byte aligned");
+  rkv_r4kv_header h = *identity;
+  h.token_start = (uint32_t)token_start;
+  h.token_count = (uint32_t)token_count;
+  h.layer_lo = (uint16_t)layer_lo;
+  h.layer_hi = (uint16_t)layer_hi;
+  h.k_fmt = RKV_FMT_Q8;
+  h.v_fmt = RKV_FMT_Q8;
+  h.payload_len = need - RKV_R4KV_HEADER_BYTES - 4;
+  h.sketch_offset = 0;
+  h.flags = (uint16_t)(identity->flags & ~1u);  // no sketch
+  rkv::R4kvLaunch r{};
+  r.g = to_geo(&p->g);
+  r.layer_stride = (int64_t)p->layer_bytes;
+  r.layer_lo = layer_lo;
+  r.n_layers = layer_hi - layer_lo + 1;
+  r.t0 = token_start;
+  r.count = token_count;
+  rkv_r4kv_header_encode(&h, r.header);
+  hipStream_t hs = as_stream(stream);
+  hipError_t e = rkv::launch_r4kv_pack(r, p->pages, p->d_tables + (size_t)seq * p->d.max_pages_per_seq,
+                                       static_cast<uint8_t *>(staging), p->d_crc, p->ctx->d_fault, hs);
+  if (e != hipSuccess) return hip_fail(op, e);
+  if (dst != staging && (e = hipMemcpyAsync(dst, staging, need, hipMemcpyDefault, hs)) != hipSuccess)
+    return hip_fail(op, e);
+  return RKV_OK;
+}
+
+rkv_status rkv_pool_restore(rkv_pool *p, int32_t seq, const uint8_t *page, size_t page_bytes,
+                            const rkv_r4kv_expect *expect, void *staging, size_t staging_bytes,
+                            int32_t *refusal, void *stream) {
+  const char *op = "rkv_pool_restore";
+  if (refusal) *refusal = RKV_R4KV_ACCEPTED;
+  if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  if (rkv_status s = check_seq(p->alloc, seq, op)) return s;
+  if (!page || !expect) return fail(RKV_ERR_INVALID_ARG, op, "NULL page/expect");
+  // host gates first: nothing reaches the device unless these pass
+  if (page_bytes < RKV_R4KV_HEADER_BYTES + 4) return refuse(refusal, RKV_R4KV_LENGTH, op, "shorter than 100 bytes");
+  rkv_r4kv_header h;
+  if (rkv_status s = rkv_r4kv_header_decode(page, &h, refusal)) return s;
+  const size_t body_len = page_bytes - RKV_R4KV_HEADER_BYTES - 4;
+  if (rkv_status s = rkv_r4kv_check_restore(&h, expect, body_len, refusal)) return s;
+  if (h.k_fmt != RKV_FMT_Q8 || h.v_fmt != RKV_FMT_Q8)
+    return fail(RKV_ERR_UNSUPPORTED, op, "k_fmt=%u v_fmt=%u (this pool holds Q8)", h.k_fmt, h.v_fmt);
+  if (h.layer_hi >= p->d.layers || h.layer_lo > h.layer_hi)
+    return fail(RKV_ERR_INVALID_ARG, op, "page layers [%u, %u] of %d", h.layer_lo, h.layer_hi, p->d.layers);
+  if (body_len != spill_body_bytes(p, h.token_count, h.layer_hi - h.layer_lo + 1))
+    return fail(RKV_ERR_INVALID_ARG, op, "body of %zu bytes does not match %u tokens x layers [%u, %u]",
+                body_len, h.token_count, h.layer_lo, h.layer_hi);
+  if ((int64_t)h.token_start + h.token_count > p->alloc->lens[seq])
+    return fail(RKV_ERR_INVALID_ARG, op, "tokens [%u, +%u) outside the %d reserved for seq %d",
+                h.token_start, h.token_count, p->alloc->lens[seq], seq);
+  if (!staging || staging_bytes < body_len || reinterpret_cast<uintptr_t>(staging) % 16 != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "staging must be 16-byte aligned and hold %zu bytes", body_len);
+  const uint32_t stored = get32(page, (int)(RKV_R4KV_HEADER_BYTES + body_len));
+  hipStream_t hs = as_stream(stream);
+  hipError_t e;
+  if (body_len > 0 &&
+      (e = hipMemcpyAsync(staging, page + RKV_R4KV_HEADER_BYTES, body_len, hipMemcpyHostToDevice, hs)) != hipSuccess)
+    return hip_fail(op, e);
+  if ((e = rkv::launch_crc32c(static_cast<const uint8_t *>(staging), (int64_t)body_len, p->d_crc, hs)) != hipSuccess ||
+      (e = hipMemcpyAsync(p->h_crc, p->d_crc, 4, hipMemcpyDeviceToHost, hs)) != hipSuccess ||
+      (e = hipStreamSynchronize(hs)) != hipSuccess)
+    return hip_fail(op, e);
+  if (*p->h_crc != stored) return refuse(refusal, RKV_R4KV_PAYLOAD_CHECKSUM, op, "payload CRC32C");
+  rkv::R4kvLaunch r{};
+  r.g = to_geo(&p->g);
+  r.layer_stride = (int64_t)p->layer_bytes;
+  r.layer_lo = h.layer_lo;
+  r.n_layers = h.layer_hi - h.layer_lo + 1;
+  r.t0 = (int32_t)h.token_start;
+  r.count = (int32_t)h.token_count;
+  if ((e = rkv::launch_r4kv_unpack(r, p->pages, p->d_tables + (size_t)seq * p->d.max_pages_per_seq,
+                                   static_cast<const uint8_t *>(staging), p->ctx->d_fault, hs)) != hipSuccess)
+    return hip_fail(op, e);
+  return RKV_OK;
 }
 
 }  // extern "C"
