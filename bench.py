@@ -62,7 +62,7 @@ def parse():
     ap.add_argument("--config", type=int, default=1,
                     help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs; "
                          "6 = prefix-shared decode (forks + copy-on-write pages); "
-                         "7 = chunked prefill attention")
+                         "7 = chunked prefill attention; 8 = R4KV page spill/restore")
     ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
     ap.add_argument("--append-launch", action="store_true",
                     help="append the step's rows with a separate rkv_pool_append launch instead "
@@ -832,8 +832,90 @@ def run_config7(args) -> int:
     return 0
 
 
+def run_config8(args) -> int:
+    """Off-HBM tier (R4KV pages): a 4096-token range of one sequence over 48
+    layers (Hkv=2, D=256, page 64) is one page of 214 MB.  Timed, with HIP
+    events: the device CRC32C over 1 GiB (its HBM roofline); spill into a
+    device staging buffer (pack + CRC, no PCIe); spill to pinned host memory
+    (+ the D2H copy); restore from pinned host memory (H2D copy, device CRC
+    check, one host wait, unpack).  `value` is the spill-to-host rate."""
+    import numpy as np
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    Hkv, D, PT, layers, T = 2, 256, 64, 48, 4096
+    pps = T // PT
+    pool = rkv.Pool(ctx, layers, Hkv, D, PT, 2 * pps + 8, 2, pps, seed=args.seed)
+    pool.alloc.reserve(0, T)
+    pool.alloc.reserve(1, T)
+    pool.sync_tables()
+    for layer in range(layers):
+        _fill_layer(rkv, pool, layer, [0], [T], Hkv, D, args.seed)
+    ctx.sync()
+    n = pool.r4kv_page_bytes(T, 0, layers - 1)
+    staging = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+    host = torch.empty(n, dtype=torch.uint8).pin_memory()
+    ident = rkv.R4kvHeader(prefix_digest=0xC0FFEE, token_start=0, token_count=T, pos_start=0,
+                           layer_lo=0, layer_hi=layers - 1, k_fmt=1, v_fmt=1, epoch=1,
+                           generation=1, payload_len=0, sketch_offset=0, flags=0)
+    exp = rkv.R4kvExpect(prefix_digest=0xC0FFEE, token_start=0, pos_start=0, layer_lo=0,
+                         layer_hi=layers - 1, k_fmt=1, v_fmt=1, check_generation=0,
+                         generation_min=0, generation_max=0)
+    stream = torch.cuda.current_stream()
+    big = torch.randint(0, 256, (1 << 30,), dtype=torch.uint8, device=dev)
+    word = torch.zeros(4, dtype=torch.int32, device=dev)
+    reps = max(args.steps // 5, 3)
+
+    def timed(fn):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps, (time.perf_counter() - t0) / reps
+
+    crc_s, _ = timed(lambda: rkv.crc32c(ctx, big, big.numel(), word, stream))
+    spill_dev_s, _ = timed(lambda: pool.spill(0, 0, T, 0, layers - 1, ident, staging, staging, stream))
+    spill_host_s, _ = timed(lambda: pool.spill(0, 0, T, 0, layers - 1, ident, staging, host, stream))
+    page = host.numpy()
+    _, restore_s = timed(lambda: pool.restore(1, page, exp, staging, stream))
+    ctx.sync()
+    res = {
+        "metric": "config 8: R4KV page spill to host GB/s (4096 tokens x 48 layers per page)",
+        "value": round(n / spill_host_s / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": reps,
+        "warmup": 2, "ms_per_step": round(spill_host_s * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "u8 (Q8_0 page bytes), CRC32C",
+        "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel)",
+        "config": {"workload": "R4KV spill/restore: one sequence, tokens [0, 4096), layers 0-47, "
+                               "Hkv=2, D=256, page 64; page = header + body + CRC32C",
+                   "page_bytes": n, "layers": layers, "tokens": T},
+        "spill_to_device_us": round(spill_dev_s * 1e6, 1),
+        "spill_to_device_gbs": round(n / spill_dev_s / 1e9, 1),
+        "spill_to_host_us": round(spill_host_s * 1e6, 1),
+        "restore_from_host_us": round(restore_s * 1e6, 1),
+        "restore_from_host_gbs": round(n / restore_s / 1e9, 2),
+        "roofline": {"bound": "hbm", "kernel": "rkv::crc32c_kernel", "achieved": round((1 << 30) / crc_s / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round((1 << 30) / crc_s / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+                     "crc_bytes": 1 << 30, "crc_us": round(crc_s * 1e6, 1)},
+    }
+    print(json.dumps(res), flush=True)
+    pool.close()
+    ctx.close()
+    return 0
+
+
 if __name__ == "__main__":
     _a = parse()
+    if _a.config == 8:
+        sys.exit(run_config8(_a))
     if _a.config == 7:
         sys.exit(run_config7(_a))
     if _a.config == 4:
