@@ -593,6 +593,8 @@ size_t rko_scale_offset(const rko_layout *L, int32_t slot, int32_t block) {
   return (size_t)L->page_tokens * (size_t)L->head_dim +
          2 * ((size_t)(slot / TT) * nb * (size_t)TT + (size_t)block * (size_t)TT + (size_t)t);
 }
+/* V codes are stored as x ^ 0x80 (unsigned x + 128), K codes as they are */
+static uint8_t v_bias(int kind) { return kind == 1 ? 0x80 : 0x00; }
 static size_t region_base(const rko_layout *L, int32_t page, int32_t kvh, int kind) {
   return (size_t)page * rko_page_bytes(L) + (size_t)(kvh * 2 + kind) * rko_region_bytes(L);
 }
@@ -622,7 +624,7 @@ int32_t rko_paged_append(const rko_layout *L, uint8_t *pages,
           reg[so] = row[b * 34];
           reg[so + 1] = row[b * 34 + 1];
           for (int32_t i = 0; i < 32; ++i)
-            reg[rko_code_offset(L, kind, slot, b * 32 + i)] = row[b * 34 + 2 + i];
+            reg[rko_code_offset(L, kind, slot, b * 32 + i)] = row[b * 34 + 2 + i] ^ v_bias(kind);
         }
       }
     }
@@ -649,7 +651,7 @@ int32_t rko_paged_gather(const rko_layout *L, const uint8_t *pages,
         row[b * 34] = reg[so];
         row[b * 34 + 1] = reg[so + 1];
         for (int32_t i = 0; i < 32; ++i)
-          row[b * 34 + 2 + i] = reg[rko_code_offset(L, kind, slot, b * 32 + i)];
+          row[b * 34 + 2 + i] = reg[rko_code_offset(L, kind, slot, b * 32 + i)] ^ v_bias(kind);
       }
     }
   }

@@ -84,7 +84,8 @@ __global__ __launch_bounds__(256) void gather_kernel(Geo g, const uint8_t *pages
   const uint16_t sc = *reinterpret_cast<const uint16_t *>(region + scale_offset(g, slot, b));
   dst[0] = (uint8_t)(sc & 0xffu);
   dst[1] = (uint8_t)(sc >> 8);
-  for (int i = 0; i < 32; ++i) dst[2 + i] = region[code_offset(g, kind, slot, b * 32 + i)];
+  const uint8_t bias = code_bias(kind);
+  for (int i = 0; i < 32; ++i) dst[2 + i] = region[code_offset(g, kind, slot, b * 32 + i)] ^ bias;
 }
 
 __global__ __launch_bounds__(256) void import_kernel(Geo g, uint8_t *pages, const int32_t *bt,
@@ -108,7 +109,8 @@ __global__ __launch_bounds__(256) void import_kernel(Geo g, uint8_t *pages, cons
   const uint8_t *src = rows + ((int64_t)kvh * len + pos) * (NB * 34) + b * 34;
   *reinterpret_cast<uint16_t *>(region + scale_offset(g, slot, b)) =
       (uint16_t)(src[0] | ((uint16_t)src[1] << 8));
-  for (int i = 0; i < 32; ++i) region[code_offset(g, kind, slot, b * 32 + i)] = src[2 + i];
+  const uint8_t bias = code_bias(kind);
+  for (int i = 0; i < 32; ++i) region[code_offset(g, kind, slot, b * 32 + i)] = src[2 + i] ^ bias;
 }
 
 __global__ __launch_bounds__(256) void f32_to_f16_kernel(const float *in, uint16_t *out, int64_t n,

@@ -30,9 +30,10 @@
 //   softmax : scores live one row per lane column; max across the 4 lane
 //             groups with two shuffles, exp2 on the VALU.
 //   PV      : O^T[dim][row] on v_mfma_f32_16x16x32_f16.  A = V codes
-//             widened int8 -> f16 exactly (bias trick: 0x6400|(x^0x80) is
-//             1024+x+128, minus 1152), B = p * d_v (the f16 V scale of that
-//             token and block) rounded once to f16; f32 accumulation.
+//             widened to f16 exactly (they are stored as x+128: 0x6400|byte
+//             is 1024+x+128, minus 1152), B = the weight p * d_v (the f16 V
+//             scale of that token and block) as two f16 terms; f32
+//             accumulation.
 #pragma once
 
 #include "rkv_launch.h"
@@ -71,9 +72,8 @@ __device__ __forceinline__ float dpp_ror8(float x) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
 }
 
-// 4 int8 codes (one dword) -> 4 exact f16 values.
-__device__ __forceinline__ void i8x4_to_f16(uint32_t w, v2h &lo, v2h &hi) {
-  const uint32_t u = w ^ 0x80808080u;  // x + 128 as unsigned bytes
+// 4 stored V codes (one dword of x + 128 bytes) -> 4 exact f16 values x.
+__device__ __forceinline__ void v8x4_to_f16(uint32_t u, v2h &lo, v2h &hi) {
   const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
   const uint32_t h = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
   const v2h bias = {(_Float16)1152.0f, (_Float16)1152.0f};
@@ -349,6 +349,7 @@ struct Decoder {
     // ---- online softmax (base 2, lazily rescaled reference max) ----
     uint32_t pp[NP][4];  // p of the lane's 8 tokens as packed f16 pairs
     uint32_t pl[NP][4];  // kSplitP: p - f16(p), rounded to f16
+    uint32_t pz[NP][4];  // kColSplit: f16(p) on lanes li >= 8, 0 on lanes li < 8
 #pragma unroll
     for (int np = 0; np < NP; ++np) {
       float s[8];
@@ -401,6 +402,12 @@ struct Decoder {
         if constexpr (kSplitP) {
           const v2h l2 = {(_Float16)(pr[2 * i] - (float)h2[0]), (_Float16)(pr[2 * i + 1] - (float)h2[1])};
           pl[np][i] = __builtin_bit_cast(uint32_t, l2);
+          if constexpr (kColSplit) {
+            // columns 0-7 take p and no second term: zero their p_lo and
+            // (below) their product subtrahend
+            pz[np][i] = li >= 8 ? pp[np][i] : 0u;
+            if (li < 8) pl[np][i] = 0u;
+          }
         }
       }
     }
@@ -423,13 +430,23 @@ struct Decoder {
         smask[i] = (tk < len ? 0xffffu : 0u) | (tk + 1 < len ? 0xffff0000u : 0u);
       }
     }
+    pv(st, pp, pl, pz, smask);
+  }
+
+  // PV of one tile (see compute); `smask` clears the V scales of tokens past
+  // the sequence end.  (A separate unmasked copy for the other tiles
+  // measured no faster.)
+  __device__ __forceinline__ void pv(const lds_u8 *st, const uint32_t (&pp)[NP][4],
+                                     const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4],
+                                     const uint32_t (&smask)[4]) {
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
       // (ext-vector loads only: an LDS load of the uint4 struct type makes the
       // compiler drain every in-flight copy before it)
       const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
-      const uint32_t sc[4] = {(uint32_t)sv[0] & smask[0], (uint32_t)sv[1] & smask[1],
-                              (uint32_t)sv[2] & smask[2], (uint32_t)sv[3] & smask[3]};
+      uint32_t sc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sc[i] = (uint32_t)sv[i] & smask[i];
       v8h pb[NP], pbl[NP];
 #pragma unroll
       for (int np = 0; np < NP; ++np) {
@@ -437,14 +454,20 @@ struct Decoder {
         for (int i = 0; i < 4; ++i) {
           const v2h ph = __builtin_bit_cast(v2h, pp[np][i]);
           const v2h dv = __builtin_bit_cast(v2h, sc[i]);
-          const v2h prod = ph * dv;
-          v2h hi = prod;
-          if constexpr (kSplitP) {
-            const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
-            const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, err);
-            if constexpr (kColSplit) {
-              if (li >= 8) hi = lo;
-            } else {
+          v2h hi;
+          if constexpr (kColSplit) {
+            // lanes li < 8: q = 0, so e = f16(p)*d_v rounded once and the
+            // second fma adds 0 * d_v; lanes li >= 8: e is the product's
+            // exact rounding error and the result the second weight term
+            const v2h q = __builtin_bit_cast(v2h, pz[np][i]) * dv;
+            const v2h e = __builtin_elementwise_fma(ph, dv, -q);
+            hi = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, e);
+          } else {
+            const v2h prod = ph * dv;
+            hi = prod;
+            if constexpr (kSplitP) {
+              const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
+              const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, err);
               pbl[np][2 * i] = lo[0];
               pbl[np][2 * i + 1] = lo[1];
             }
@@ -460,8 +483,8 @@ struct Decoder {
         const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * lg);
         const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * lg);
         v2h a0, a1, a2, a3;
-        i8x4_to_f16(w0, a0, a1);
-        i8x4_to_f16(w1, a2, a3);
+        v8x4_to_f16(w0, a0, a1);
+        v8x4_to_f16(w1, a2, a3);
         const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
 #pragma unroll
         for (int np = 0; np < NP; ++np) {

@@ -16,7 +16,8 @@ namespace rkv {
 //   page   = [kv_head][kind K|V][region]
 //   region = codes (page_tokens*D bytes) then scales (page_tokens*D/32 f16)
 //   K codes : [slot][dim]                     -- the reference row order
-//   V codes : [slot/TT][dim][slot%TT]         -- dim-major inside 32-slot tiles
+//   V codes : [slot/TT][dim][slot%TT]         -- dim-major inside 32-slot tiles,
+//                                                stored as x ^ 0x80 (code_bias)
 //   scales  : [slot/TT][block][sigma(slot%TT)] -- K and V alike
 // with TT = min(32, page_tokens).  Inside a 32-slot tile the scales are kept
 // in the order the decode kernel's lanes consume them: slot t = 16*m + 4*g + r
@@ -50,6 +51,10 @@ __host__ __device__ inline uint64_t region_base(const Geo &g, int32_t page, int3
                                                 int32_t kind) {
   return (uint64_t)page * page_bytes(g) + (uint64_t)(kvh * 2 + kind) * region_bytes(g);
 }
+// V codes are stored biased, as x ^ 0x80 (x + 128 as an unsigned byte): the
+// decode widens them to f16 with two byte permutes and no sign flip.  K codes
+// are stored as they are (the int8 MFMA reads them).
+__host__ __device__ constexpr uint8_t code_bias(int32_t kind) { return kind == 1 ? 0x80 : 0x00; }
 // byte offset of code (slot, dim) inside a region of `kind`
 __host__ __device__ inline uint32_t code_offset(const Geo &g, int32_t kind, int32_t slot,
                                                 int32_t dim) {
@@ -221,7 +226,8 @@ __device__ inline void store_q8_lane(const Geo &g, uint8_t *region, int32_t kind
     *reinterpret_cast<uint32_t *>(region + code_offset(g, 0, slot, dim0)) = codes;
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) region[code_offset(g, 1, slot, dim0 + i)] = (uint8_t)(codes >> (8 * i));
+    for (int i = 0; i < 4; ++i)
+      region[code_offset(g, 1, slot, dim0 + i)] = (uint8_t)(codes >> (8 * i)) ^ code_bias(1);
   }
   if (sub == 0) *reinterpret_cast<uint16_t *>(region + scale_offset(g, slot, blk)) = scale;
 }

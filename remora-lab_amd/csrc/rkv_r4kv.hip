@@ -116,7 +116,8 @@ __global__ __launch_bounds__(256) void pack_kernel(BodyMap m, const uint8_t *pag
   const uint16_t sc = *reinterpret_cast<const uint16_t *>(region + scale_offset(m.g, slot, b));
   dst[0] = (uint8_t)(sc & 0xffu);
   dst[1] = (uint8_t)(sc >> 8);
-  for (int i = 0; i < 32; ++i) dst[2 + i] = region[code_offset(m.g, kind, slot, b * 32 + i)];
+  const uint8_t bias = code_bias(kind);
+  for (int i = 0; i < 32; ++i) dst[2 + i] = region[code_offset(m.g, kind, slot, b * 32 + i)] ^ bias;
 }
 
 __global__ __launch_bounds__(256) void unpack_kernel(BodyMap m, uint8_t *pages, const int32_t *bt,
@@ -142,7 +143,8 @@ __global__ __launch_bounds__(256) void unpack_kernel(BodyMap m, uint8_t *pages, 
   const uint8_t *src = body + tid * 34;
   *reinterpret_cast<uint16_t *>(region + scale_offset(m.g, slot, b)) =
       (uint16_t)(src[0] | ((uint16_t)src[1] << 8));
-  for (int i = 0; i < 32; ++i) region[code_offset(m.g, kind, slot, b * 32 + i)] = src[2 + i];
+  const uint8_t bias = code_bias(kind);
+  for (int i = 0; i < 32; ++i) region[code_offset(m.g, kind, slot, b * 32 + i)] = src[2 + i] ^ bias;
 }
 
 // The 96 header bytes (already serialized on the host) at the page start,
