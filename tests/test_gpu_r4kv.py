@@ -160,3 +160,35 @@ def test_restore_round_trip_and_refusals(rkv, rko, ctx):
     ctx.sync()
     assert again.cpu().numpy().tobytes() == page_bytes
     pool.close()
+
+
+@pytest.mark.parametrize("D,PT,t0,count", [(256, 64, 37, 150), (128, 16, 5, 40), (256, 32, 33, 1)])
+def test_restore_partial_tiles_keep_neighbours(rkv, rko, ctx, D, PT, t0, count):
+    """A range that starts and ends inside page tiles: restoring seq 0's rows
+    into seq 1 replaces exactly [t0, t0+count) of seq 1 on every layer and
+    leaves its other rows (same tiles included) byte-identical."""
+    torch = _torch()
+    Hkv, layers = 2, 2
+    pool = _filled_pool(rkv, ctx, layers, Hkv, D, PT, [300, 300], seed=PT + t0)
+    n = pool.r4kv_page_bytes(count, 0, layers - 1)
+    staging = torch.zeros(n + 64, dtype=torch.uint8, device="cuda")
+    page = torch.zeros(n, dtype=torch.uint8).pin_memory()
+    pool.spill(0, t0, count, 0, layers - 1, _identity(rkv, pos_start=t0), staging, page)
+    ctx.sync()
+    before = _oracle_body(rkv, rko, pool, 1, 0, 300, 0, layers - 1)
+    src = _oracle_body(rkv, rko, pool, 0, 0, 300, 0, layers - 1)
+    exp = rkv.R4kvExpect(prefix_digest=0x1234ABCD5678EF01, token_start=t0, pos_start=t0,
+                         layer_lo=0, layer_hi=layers - 1, k_fmt=-1, v_fmt=-1, check_generation=0,
+                         generation_min=0, generation_max=0)
+    pool.restore(1, page.numpy().tobytes(), exp, staging)
+    ctx.sync()
+    after = _oracle_body(rkv, rko, pool, 1, 0, 300, 0, layers - 1)
+    rb = D // 32 * 34
+    shape = (layers, 2, Hkv, 300, rb)
+    b = np.frombuffer(before, np.uint8).reshape(shape)
+    a = np.frombuffer(after, np.uint8).reshape(shape)
+    s = np.frombuffer(src, np.uint8).reshape(shape)
+    assert np.array_equal(a[:, :, :, t0:t0 + count], s[:, :, :, t0:t0 + count])
+    assert np.array_equal(a[:, :, :, :t0], b[:, :, :, :t0])
+    assert np.array_equal(a[:, :, :, t0 + count:], b[:, :, :, t0 + count:])
+    pool.close()
