@@ -208,7 +208,11 @@ __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "mem
 // stages and meet at two barriers per tile (stage free, tile landed).
 // kPageList: page ids come from a workgroup list in LDS (any length) instead
 // of one register lane per page (at most 64 pages).
-template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kPageList = false>
+// kF16V: after a tile lands the waves widen its V codes to f16 once, each
+// its share, into an LDS tile laid out as the PV MFMA's A operand (one
+// 16-byte read per operand); without it every wave widens the whole tile.
+template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kPageList = false,
+          bool kF16V = false>
 struct Decoder {
   using S = StageShape<D>;
   static constexpr bool kSplitP = true;    // two-term f16 PV weights (see compute)
@@ -227,6 +231,7 @@ struct Decoder {
   int32_t pg_first;        // first page index (within the sequence) of the partition
   int32_t pidv;            // lane i: page id of the partition's i-th page
   const __attribute__((address_space(3))) int32_t *pg_lds;  // kPageList: page id of page index i
+  lds_u8 *vf16;            // kF16V: [dim][4 k-groups] x 8 f16, k-group slot lg ^ (dim & 3)
   const uint8_t *kv_base;  // pages + kv head offset
   uint64_t PB;
   ChunkPlan<D, kSmall> plan;
@@ -480,12 +485,17 @@ struct Decoder {
       for (int hm = 0; hm < 2; ++hm) {
         const int d = 32 * blk + 16 * hm + li;
         const int sw = (d >> 2) & 1;
-        const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * lg);
-        const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * lg);
-        v2h a0, a1, a2, a3;
-        v8x4_to_f16(w0, a0, a1);
-        v8x4_to_f16(w1, a2, a3);
-        const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        v8h va;
+        if constexpr (kF16V) {
+          va = lds_load<v8h>(vf16 + 16 * (4 * d + (lg ^ (d & 3))));
+        } else {
+          const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * lg);
+          const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * lg);
+          v2h a0, a1, a2, a3;
+          v8x4_to_f16(w0, a0, a1);
+          v8x4_to_f16(w1, a2, a3);
+          va = v8h{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        }
 #pragma unroll
         for (int np = 0; np < NP; ++np) {
           oacc[np][2 * blk + hm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[np], oacc[np][2 * blk + hm], 0, 0, 0);
@@ -515,12 +525,35 @@ struct Decoder {
   }
 
   // Tile t: prefetch tile t+NS-1 into `fill`, wait for `cur`, compute it.
+  // kF16V: widen this wave's share of the landed tile's V codes into vf16.
+  // Chunk (dim d, k-group g) is the 8 tokens lane (d, g) of the PV MFMA
+  // holds: 4g..4g+3 then 16+4g..16+4g+3 (the halves are swapped in the
+  // stage when (d >> 2) & 1, as the tile copy put them).
+  __device__ __forceinline__ void widen_v(const lds_u8 *st) {
+    constexpr int kChunks = 4 * D;
+    for (int c = wave * 64 + lane; c < kChunks; c += 64 * NW) {
+      const int d = c >> 2, g = c & 3;
+      const int sw = (d >> 2) & 1;
+      const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * g);
+      const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * g);
+      v2h a0, a1, a2, a3;
+      v8x4_to_f16(w0, a0, a1);
+      v8x4_to_f16(w1, a2, a3);
+      const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+      *reinterpret_cast<__attribute__((address_space(3))) v8h *>(vf16 + 16 * (4 * d + (g ^ (d & 3)))) = va;
+    }
+  }
+
   __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
-    if (NW > 1) wg_barrier();  // every wave is done with `fill` (tile t-1)
+    if (NW > 1) wg_barrier();  // every wave is done with `fill` (tile t-1) and vf16
     if (t + NS - 1 < n_tiles) issue(t + NS - 1, fill);
     const int ahead = min(n_tiles - 1 - t, NS - 1);
     wait_tiles_ahead(ahead);
     if (NW > 1) wg_barrier();  // every wave's copies of tile t have landed
+    if constexpr (kF16V) {
+      widen_v(cur);
+      wg_barrier();  // vf16 holds tile t
+    }
     compute(t, cur);
   }
 

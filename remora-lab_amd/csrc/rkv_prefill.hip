@@ -10,9 +10,11 @@
 // LDS is read from memory once per 128 rows.  Wave w owns rows 16w..16w+15;
 // the per-tile work (int8 QK MFMA with exact K dequant, base-2 online
 // softmax, f16 PV MFMA) is the decode kernel's, with the causal limit of
-// every row at ctx + its token + 1.  The block walks its whole causal range
-// [0, ctx + last token of the block], with the range's page ids staged in
-// an LDS list.  Output rows are written normalized; no workspace.
+// every row at ctx + its token + 1; the V codes of each tile are widened to
+// f16 once per workgroup (each wave its share) instead of once per wave.
+// The block walks its whole causal range [0, ctx + last token of the
+// block], with the range's page ids staged in an LDS list.  Output rows are
+// written normalized; no workspace.
 #include "rkv_decode_kernel.h"
 
 namespace rkv {
@@ -21,10 +23,11 @@ namespace {
 template <int D, bool kSmall, int NS>
 __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillLaunch pf) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using Dec = Decoder<D, 2, kSmall, NS, kPrefillWaves, true>;
+  using Dec = Decoder<D, 2, kSmall, NS, kPrefillWaves, true, true>;
   using S = StageShape<D>;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
   __shared__ int32_t page_list[kPrefillMaxPages];
+  __shared__ __attribute__((aligned(16))) uint8_t v_f16[D * 64];  // the tile's V as f16
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
@@ -77,6 +80,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillL
   dc.pg_first = 0;
   dc.pidv = 0;
   dc.pg_lds = (const __attribute__((address_space(3))) int32_t *)page_list;
+  dc.vf16 = (lds_u8 *)v_f16;
 
   const int32_t G = p.q_heads / g.kv_heads;  // rows of one chunk token
   // row r of the block: chunk token j0 + r / G, q head kvh*G + r % G
