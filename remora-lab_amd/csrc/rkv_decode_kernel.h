@@ -53,14 +53,15 @@ constexpr int kTile = 32;    // tokens per tile
 constexpr int kWaitBase = 0x0f70;
 
 // LDS stage: [K codes 32*D][K scales 2*D][V codes 32*D][V scales 2*D],
-// padded to whole 1 KiB global_load_lds instructions.
-template <int D>
+// padded to whole 1 KiB global_load_lds instructions.  kKReg: the K codes
+// go to registers instead, and the stage is [V codes][K scales][V scales].
+template <int D, bool kKReg = false>
 struct StageShape {
   static constexpr int kKC = 0;
   static constexpr int kKS = 32 * D;
-  static constexpr int kVC = 34 * D;
-  static constexpr int kVS = 66 * D;
-  static constexpr int kBytes = 68 * D;
+  static constexpr int kVC = kKReg ? 0 : 34 * D;
+  static constexpr int kVS = kKReg ? 34 * D : 66 * D;
+  static constexpr int kBytes = kKReg ? 36 * D : 68 * D;
   static constexpr int kChunks = kBytes / 16;
   static constexpr int kInstr = (kChunks + 63) / 64;
   static constexpr int kAlloc = kInstr * 1024;
@@ -98,9 +99,9 @@ __device__ __forceinline__ v4f f16x4_to_f32(uint2 w) {
 // 16-token pages hold half a tile each: the code runs are still 16-byte
 // copies, but the lane-ordered scale runs interleave the two pages every 4
 // bytes, so they use 4-byte copies.
-template <int D, bool kSmallPage>
+template <int D, bool kSmallPage, bool kKReg = false>
 struct ChunkPlan {
-  using S = StageShape<D>;
+  using S = StageShape<D, kKReg>;
   static constexpr int kNKC = D / 32;                       // 1 KiB K-code (or V-code) copies
   static constexpr int kN16 = kSmallPage ? 2 * kNKC : S::kInstr;
   static constexpr int kN4 = kSmallPage ? 2 * (D / 128) : 0;  // 256-byte scale copies
@@ -116,14 +117,37 @@ struct ChunkPlan {
   }
 };
 
-template <int D, bool kSmallPage>
-__device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage> &pl, const Geo &g, int lane) {
-  using S = StageShape<D>;
-  using PL = ChunkPlan<D, kSmallPage>;
+template <int D, bool kSmallPage, bool kKReg = false>
+__device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage, kKReg> &pl, const Geo &g,
+                                          int lane) {
+  using S = StageShape<D, kKReg>;
+  using PL = ChunkPlan<D, kSmallPage, kKReg>;
   const uint32_t RB = (uint32_t)region_bytes(g);
   const uint32_t PTD = (uint32_t)g.page_tokens * D;
   pl.halves = 0;
-  if constexpr (!kSmallPage) {
+  if constexpr (kKReg) {
+    static_assert(!kSmallPage, "K codes in registers need 32-token tiles in one page");
+#pragma unroll
+    for (int k = 0; k < S::kInstr; ++k) {
+      const int c = 64 * k + lane;
+      uint32_t off = 0, is_scale = 0;
+      if (c < 2 * D) {  // V codes: dim row d, 16-token piece (halves swapped when (d>>2)&1)
+        const int d = c >> 1;
+        const int lh = (c & 1) ^ ((d >> 2) & 1);
+        off = RB + (uint32_t)(d * 32 + 16 * lh);
+      } else if (c < 2 * D + D / 8) {  // K scales
+        const int i = c - 2 * D;
+        off = PTD + 2u * (uint32_t)(32 * (i >> 2) + 8 * (i & 3));
+        is_scale = 1;
+      } else if (c < 2 * D + D / 4) {  // V scales
+        const int i = c - (2 * D + D / 8);
+        off = RB + PTD + 2u * (uint32_t)(32 * (i >> 2) + 8 * (i & 3));
+        is_scale = 1;
+      }  // else: padding lane of the last copy, re-reads chunk 0 of the tile
+      pl.off[k] = off;
+      pl.mul[k] = is_scale ? (uint32_t)(D / 16) : (uint32_t)D;
+    }
+  } else if constexpr (!kSmallPage) {
 #pragma unroll
     for (int k = 0; k < S::kInstr; ++k) {
       const int c = 64 * k + lane;
@@ -211,10 +235,15 @@ __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "mem
 // kF16V: after a tile lands the waves widen its V codes to f16 once, each
 // its share, into an LDS tile laid out as the PV MFMA's A operand (one
 // 16-byte read per operand); without it every wave widens the whole tile.
+// kKReg (one wave, pages of >= 32 tokens): each tile's K codes are loaded
+// straight into the QK MFMA's A-operand registers (8 x 16 bytes per lane,
+// 16 rows x 64 contiguous bytes per load) instead of through the LDS stage;
+// the next tile's are loaded as soon as this tile's QK has read them.  The
+// stage then holds only V codes and the scales, 9 KiB at D=256.
 template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kPageList = false,
-          bool kF16V = false>
+          bool kF16V = false, bool kKReg = false>
 struct Decoder {
-  using S = StageShape<D>;
+  using S = StageShape<D, kKReg>;
   static constexpr bool kSplitP = true;    // two-term f16 PV weights (see compute)
   // With one QK n-tile (at most 8 rows) the PV MFMA's columns 8-15 are free:
   // they carry the second weight term of rows 0-7 instead of a second MFMA,
@@ -234,7 +263,8 @@ struct Decoder {
   lds_u8 *vf16;            // kF16V: [dim][4 k-groups] x 8 f16, k-group slot lg ^ (dim & 3)
   const uint8_t *kv_base;  // pages + kv head offset
   uint64_t PB;
-  ChunkPlan<D, kSmall> plan;
+  ChunkPlan<D, kSmall, kKReg> plan;
+  v4i kreg[2][D / 64];     // kKReg: K codes of the tile being computed (A operands)
   v4i qhi[NT][NC], qlo[NT][NC];
   float rmul[NP];
   int32_t rlim[NP];
@@ -249,7 +279,7 @@ struct Decoder {
     const Geo &g = p.g;
     const int32_t t0 = tok0 + tile * kTile;
     const int32_t pi = t0 / g.page_tokens - pg_first;
-    using PL = ChunkPlan<D, kSmall>;
+    using PL = ChunkPlan<D, kSmall, kKReg>;
     if constexpr (!kSmall) {
       const int32_t pid = kPageList ? __builtin_amdgcn_readfirstlane(pg_lds[pi])
                                     : __builtin_amdgcn_readlane(pidv, pi);
@@ -258,7 +288,10 @@ struct Decoder {
 #pragma unroll
       for (int k = 0; k < PL::kN16; ++k) {
         if (NW > 1 && k % NW != wave) continue;
-        const uint32_t voff = plan.off[k] + s0 * plan.mul[k];
+        // kKReg: copies 0..2D/64-1 are V codes, the rest scales (their
+        // padding lanes read inside the region either way)
+        const uint32_t mul = kKReg ? (64 * k < 2 * D ? (uint32_t)D : (uint32_t)(D / 16)) : plan.mul[k];
+        const uint32_t voff = plan.off[k] + s0 * mul;
         __builtin_amdgcn_global_load_lds(base + voff, dst + PL::dst16(k), 16, 0, 0);
       }
     } else {
@@ -316,8 +349,24 @@ struct Decoder {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  // Scores, online softmax and PV for the tile held in LDS stage `st`.
-  __device__ __forceinline__ void compute(int tile, const lds_u8 *st) {
+  // kKReg: K codes of tile `tile` into kreg.  Lane (li, lg) of M-tile mt,
+  // 64-dim step c holds token row 16*mt + li, dims 64*c + 16*lg .. +15.
+  __device__ __forceinline__ void load_k(int tile) {
+    const Geo &g = p.g;
+    const int32_t t0 = tok0 + tile * kTile;
+    const int32_t pid = __builtin_amdgcn_readlane(pidv, t0 / g.page_tokens - pg_first);
+    const uint8_t *base = kv_base + (uint64_t)pid * PB +
+                          (uint64_t)((t0 % g.page_tokens) + li) * D + 16 * lg;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        kreg[mt][c] = *reinterpret_cast<const v4i *>(base + (uint64_t)(16 * mt) * D + 64 * c);
+  }
+
+  // Scores, online softmax and PV for the tile held in LDS stage `st`
+  // (kKReg: the next tile is copied into `next_stage` meanwhile).
+  __device__ __forceinline__ void compute(int tile, const lds_u8 *st, lds_u8 *next_stage = nullptr) {
     const int32_t t0 = tok0 + tile * kTile;
     // ---- QK^T: int32 block dots, scaled by the f16 K scale of (token, block) ----
     float sacc[NT][2][4];
@@ -333,7 +382,7 @@ struct Decoder {
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const int pc = (4 * c + lg) ^ (krow & (S::kCPR - 1));
-        const v4i a = lds_load<v4i>(st + S::kKC + krow * D + 16 * pc);
+        const v4i a = kKReg ? kreg[mt][c] : lds_load<v4i>(st + S::kKC + krow * D + 16 * pc);
         const int blk = 2 * c + (li >> 3);
         // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
         const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
@@ -348,6 +397,19 @@ struct Decoder {
           for (int r = 0; r < 4; ++r)
             sacc[nt][mt][r] = __builtin_fmaf((float)((ch[r] << 7) + cl[r]), dk[r], sacc[nt][mt][r]);
         }
+      }
+    }
+
+    // kKReg: the QK above has read this tile's K codes and K scales; the
+    // next tile's K codes and stage copy start now and land during this
+    // tile's softmax and PV.  (They cannot start earlier: before a register
+    // use of loaded data the compiler waits for every outstanding load,
+    // stage copies included, so copies issued before a QK complete before
+    // it.)
+    if constexpr (kKReg) {
+      if (tile + 1 < n_tiles) {
+        issue(tile + 1, next_stage);
+        load_k(tile + 1);
       }
     }
 
@@ -511,7 +573,7 @@ struct Decoder {
   // waves; counting floor(kInstr / NW) per tile is exact for the waves with
   // that many and waits one copy longer for the others.
   __device__ __forceinline__ static void wait_tiles_ahead(int ahead) {
-    constexpr int kI = ChunkPlan<D, kSmall>::kInstr / NW;
+    constexpr int kI = ChunkPlan<D, kSmall, kKReg>::kInstr / NW;
     static_assert(kI >= 1, "every wave issues at least one copy per tile");
     if (ahead >= 2) {
       constexpr int n = 2 * kI;
@@ -545,6 +607,12 @@ struct Decoder {
   }
 
   __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
+    if constexpr (kKReg) {
+      // tile t's K codes and stage copy were the last loads issued
+      __builtin_amdgcn_s_waitcnt(kWaitBase);
+      compute(t, cur, fill);
+      return;
+    }
     if (NW > 1) wg_barrier();  // every wave is done with `fill` (tile t-1) and vf16
     if (t + NS - 1 < n_tiles) issue(t + NS - 1, fill);
     const int ahead = min(n_tiles - 1 - t, NS - 1);
@@ -570,8 +638,11 @@ struct Decoder {
       if (NW > 1) wg_barrier();
     }
     if (n_tiles > 0) issue(0, s0);
-    if constexpr (NS == 3) {
+    if constexpr (NS == 3 && !kKReg) {
       if (n_tiles > 1) issue(1, s1);
+    }
+    if constexpr (kKReg) {
+      if (n_tiles > 0) load_k(0);
     }
     if (app_mode == 2 && wave == 0) append_rows();
     if constexpr (NS == 2) {
@@ -810,8 +881,12 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
 template <int D, int NT, bool kSmall, int NS, int NW = 1>
 __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using Dec = Decoder<D, NT, kSmall, NS, NW>;
-  using S = StageShape<D>;
+  // single-wave workgroups over pages of >= 32 tokens with the two-stage
+  // ring take the K codes straight to registers (compute copies tile t+1
+  // into the stage tile t-1 used)
+  constexpr bool kKReg = NW == 1 && !kSmall && NS == 2;
+  using Dec = Decoder<D, NT, kSmall, NS, NW, false, false, kKReg>;
+  using S = typename Dec::S;
   constexpr int NP = Dec::NP;
   constexpr int NC = Dec::NC;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
@@ -915,7 +990,7 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     for (int m = 0; m < D / 16; ++m) dc.oacc[np][m] = v4f{0.f, 0.f, 0.f, 0.f};
   }
 
-  make_plan<D, kSmall>(dc.plan, g, lane);
+  make_plan<D, kSmall, kKReg>(dc.plan, g, lane);
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
   // The partition's page ids, one per lane (partitions start on a page

@@ -142,6 +142,9 @@ hipError_t launch_decode_rows32(const DecodeLaunch &d, hipStream_t s);
 //  - registers: head_dim 256, or more than 16 rows per kv head, takes more
 //    than half of a SIMD's 512 VGPR+AGPR per lane (one wave per SIMD);
 //    smaller shapes fit two waves per SIMD.
+// The 2-stage, <= 16-row kernel on pages of >= 32 tokens keeps K codes in
+// registers and stages only 36*head_dim bytes; registers bind before LDS for
+// both stage sizes, so the count is the same.
 constexpr int decode_wgs_per_cu(int head_dim, int rows, int stages) {
   const int stage = (68 * head_dim / 16 + 63) / 64 * 1024;
   const int by_lds = 160 * 1024 / (stages * stage);

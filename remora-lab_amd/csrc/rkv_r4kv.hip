@@ -2,16 +2,17 @@
 // CRC32C (har/crates/r4kv/src/crc32c.rs) and the pack/unpack of a token
 // range of Q8_0 rows between the page pool and a page payload.
 //
-// CRC32C.  Each wave covers a 64 KiB segment; the segments are laid out
+// CRC32C.  Each wave covers a 128 KiB segment; the segments are laid out
 // back from the end of the 16-byte-aligned prefix, so the first may start
 // before byte 0 (those leading bytes read as zero, which leaves the raw CRC
 // unchanged) and every 16-byte piece is aligned.  Lane l folds the pieces
 // l, l+64, ... of its segment (Horner: shift the running value 1024 bytes,
-// xor the piece's raw CRC from the slicing tables), the lanes combine in a
-// 6-level tree of shifts by 16*2^j bytes, and the wave's value is shifted
-// to the end of the message and xor-ed into the output word.  Wave 0 also
-// adds the raw CRC of the unaligned tail and the init/final-xor term.
-// Reads stay inside [0, n).
+// xor the piece's raw CRC from the slicing tables), and the lanes combine
+// in a 6-level tree of shifts by 16*2^j bytes.  The four waves of a block
+// hold consecutive segments: each is shifted to the block's end and xor-ed
+// in LDS, and the block's value is shifted once to the end of the message
+// and xor-ed into the output word.  Block 0 also adds the raw CRC of the
+// unaligned tail and the init/final-xor term.  Reads stay inside [0, n).
 #include "rkv_crc32c.h"
 #include "rkv_launch.h"
 
