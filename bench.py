@@ -70,6 +70,10 @@ def parse():
     ap.add_argument("--cpu-sample-seqs", type=int, default=4,
                     help="sequences of the oracle CPU baseline sample (0 = skip)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-stream-ceiling", dest="stream_ceiling", action="store_false",
+                    help="skip the streaming-read ceiling measured after the headline")
+    ap.add_argument("--graph", action="store_true",
+                    help="configs 2 and 3: report graph replays as the step time (default: eager)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 2 GiB device copy (rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE "
                          "calibration of known bytes)")
@@ -234,6 +238,8 @@ def main() -> int:
                       "decode": round(1e6 * dec_s, 2),
                       "combine": round(1e6 * sum(t_cmb) / len(t_cmb), 2),
                       "event_step": round(1e6 * sum(t_step) / len(t_step), 2),
+                      "decode_p10_p50_p90": _pcts(t_dec),
+                      "event_step_p10_p50_p90": _pcts(t_step),
                       "sampled_steps": len(sampled), "sampled_every": args.event_every},
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
@@ -243,6 +249,13 @@ def main() -> int:
                      "traffic": read_traffic(), "algorithmic_bytes_per_launch": dec_bytes},
     }
 
+    # ---- practical ceiling: a plain streaming read of HBM in the same run ---------
+    if args.stream_ceiling:
+        ceil = stream_ceiling(rkv, ctx, stream)
+        res["stream_read_ceiling"] = ceil
+        best = max(ceil["vector_gbs"], ceil["lds_dma_gbs"])
+        res["roofline"]["frac_of_stream_ceiling"] = round(res["roofline"]["achieved"] / best, 4)
+
     # ---- CPU baseline: the reference path restated in C, timed on a sample -------
     if args.cpu_sample_seqs > 0:
         res["cpu_baseline"] = cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv,
@@ -251,6 +264,42 @@ def main() -> int:
     pool.close()
     ctx.close()
     return 0
+
+
+def _pcts(xs):
+    """p10, median and p90 of a list of seconds, in microseconds."""
+    import numpy as np
+    return [round(1e6 * float(v), 2) for v in np.percentile(np.asarray(xs), [10, 50, 90])]
+
+
+def stream_ceiling(rkv, ctx, stream, nbytes=4 << 30, reps=5):
+    """Read rate of a plain stream over `nbytes` of HBM (rkv_stream_read):
+    16-byte vector loads over several grid sizes, and 1 KiB LDS-DMA copies
+    (the decode's stage copy, 16 KiB in flight per one-wave workgroup).  The
+    best grid's median over `reps` launches, in GB/s."""
+    import torch
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    word = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+
+    def rate(mode, blocks):
+        rkv.stream_read(ctx, buf, mode, blocks, word, stream=stream)  # warm
+        for r in range(reps):
+            ev[2 * r].record(stream)
+            rkv.stream_read(ctx, buf, mode, blocks, word, stream=stream)
+            ev[2 * r + 1].record(stream)
+        torch.cuda.synchronize()
+        ts = sorted(ev[2 * r].elapsed_time(ev[2 * r + 1]) * 1e-3 for r in range(reps))
+        return nbytes / ts[reps // 2] / 1e9
+
+    vec = {b: rate(0, b) for b in (256, 512, 1024, 2048)}
+    dma = {b: rate(1, b) for b in (1024, 2048, 4096)}
+    bv = max(vec, key=vec.get)
+    bd = max(dma, key=dma.get)
+    del buf
+    return {"bytes": nbytes, "vector_gbs": round(vec[bv], 1), "vector_blocks": bv,
+            "lds_dma_gbs": round(dma[bd], 1), "lds_dma_blocks": bd,
+            "kernel": "rkv_stream_read (rkv_stream.hip)"}
 
 
 def read_traffic():
@@ -437,6 +486,30 @@ def _time_steps(args, stream, step, n_events=2):
     return wall, dec
 
 
+def _time_graphs(args, dec, layers):
+    """Capture one decode step per layer pool into a HIP graph and time
+    args.steps replays (layers in rotation) by wall clock, per step."""
+    import torch
+    dec.a.split_event = None
+    torch.cuda.synchronize()
+    graphs = []
+    for layer in range(layers):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            dec.pool.decode(layer, dec.a, stream=torch.cuda.current_stream())
+        graphs.append(g)
+    for i in range(args.warmup):
+        graphs[i % layers].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        graphs[i % layers].replay()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    del graphs
+    return wall
+
+
 def run_config(args) -> int:
     """Configs 2, 3 and 5: every sequence keeps its length across steps (the
     appended rows overwrite the same slots), pools rotate over `layers` so the
@@ -515,6 +588,15 @@ def run_config(args) -> int:
 
     wall, dec_s = _time_steps(args, stream, step)
     ctx.sync()
+    launch = "eager"
+    graph_wall = None
+    if cfg in (2, 3):
+        # the same step as one HIP graph per layer pool (append + decode +
+        # combine), replayed in rotation; it measures slower than the eager
+        # launches here, so it is reported beside them and used with --graph
+        graph_wall = _time_graphs(args, dec, layers)
+        if args.graph:
+            wall, launch = graph_wall, "hip graph per layer pool, replayed"
     pt = dec.partition_tokens()
     n_parts = int(sum((int(c) + pt - 1) // pt for c in cap))  # partitions of the batch
     row = D // 32 * 34
@@ -528,7 +610,8 @@ def run_config(args) -> int:
     _line(args, cfg, work, wall, dec_s, step_bytes, step_bytes, flops,
           {"config": {"batch": B, "q_len": q_len, "layers_rotated": layers,
                       "partition_tokens": pt, "partitions_total": n_parts,
-                      "pool_pages_per_layer": num_pages},
+                      "pool_pages_per_layer": num_pages, "launch": launch},
+           **({"graph_us_per_step": round(graph_wall * 1e6, 2)} if graph_wall else {}),
            "split_k_partial_bytes": n_parts * q_len * Hq * (D + 2) * 4,
            **({"mean_accept": float(np.mean(accepts))} if accepts else {})})
     pool.close()

@@ -462,6 +462,25 @@ rkv_status rkv_pool_restore(rkv_pool *pool, int32_t seq, const uint8_t *page, si
                             const rkv_r4kv_expect *expect, void *staging, size_t staging_bytes,
                             int32_t *refusal, void *stream);
 
+/* ---- measurement --------------------------------------------------------
+ * HBM streaming-read ceiling.  No counterpart in the reference: it gives the
+ * practical read rate that the decode's bandwidth is set against, measured
+ * in the same run.  Reads the `bytes` device bytes at `data` once (16-byte
+ * aligned, bytes a multiple of 16) with `blocks` workgroups:
+ *   mode 0: 1024-thread workgroups, each wave reading 16 KiB contiguous per
+ *           round with 16-byte vector loads, the grid's waves taking the
+ *           rounds in turn; *out (device word) receives the xor of every
+ *           32-bit word read;
+ *   mode 1: one-wave workgroups, workgroup b streaming the b-th of `blocks`
+ *           equal contiguous chunks with 1 KiB LDS-DMA copies (the decode's
+ *           order and stage copy), 16 KiB in flight per wave; bytes must be
+ *           a multiple of blocks * RKV_STREAM_DMA_UNIT; `out` is not written.
+ * Both modes read with the nontemporal cache policy, as the decode does.
+ * blocks in [1, 2^20].  Stream-ordered. */
+#define RKV_STREAM_DMA_UNIT 16384
+rkv_status rkv_stream_read(rkv_ctx *ctx, const void *data, uint64_t bytes, int32_t mode,
+                           int32_t blocks, uint32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -172,6 +172,7 @@ _SIGS = {
                                    C.POINTER(R4kvHeader), P, C.c_size_t, P, C.c_size_t, P]),
     "rkv_pool_restore": (C.c_int32, [P, C.c_int32, P, C.c_size_t, C.POINTER(R4kvExpect), P,
                                      C.c_size_t, I32P, P]),
+    "rkv_stream_read": (C.c_int32, [P, P, C.c_uint64, C.c_int32, C.c_int32, P, P]),
 }
 
 _lib = None
@@ -416,6 +417,18 @@ def crc32c_host(data) -> int:
 def crc32c(ctx: Ctx, data, n: int, out, stream=None) -> None:
     """CRC32C of n bytes of a device tensor into the int32 device tensor `out`."""
     check(lib().rkv_crc32c(ctx.h, _ptr(data), n, _ptr(out), _stream(stream)))
+
+
+STREAM_DMA_UNIT = 16384
+
+
+def stream_read(ctx: Ctx, data, mode: int, blocks: int, out=None, nbytes=None, stream=None) -> None:
+    """Read the device tensor `data` once (the streaming-read ceiling):
+    mode 0 vector loads, xor of its 32-bit words into the int32 device
+    tensor `out`; mode 1 LDS-DMA copies (out unused)."""
+    n = data.numel() * data.element_size() if nbytes is None else nbytes
+    check(lib().rkv_stream_read(ctx.h, _ptr(data), n, mode, blocks,
+                                _ptr(out) if out is not None else None, _stream(stream)))
 
 
 class R4kvRefused(RkvError):

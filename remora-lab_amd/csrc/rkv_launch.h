@@ -133,6 +133,12 @@ hipError_t launch_r4kv_pack(const R4kvLaunch &r, const uint8_t *pages, const int
                             uint8_t *page_out, uint32_t *crc_word, int32_t *fault, hipStream_t s);
 hipError_t launch_r4kv_unpack(const R4kvLaunch &r, uint8_t *pages, const int32_t *bt,
                               const uint8_t *body, int32_t *fault, hipStream_t s);
+// HBM streaming-read ceiling (rkv_stream.hip): mode 0 vector loads with the
+// xor of the words read into *out, mode 1 LDS-DMA copies of
+// stream_read_dma_unit() bytes per wave round
+hipError_t launch_stream_read(const uint8_t *data, int64_t bytes, int32_t mode, int32_t blocks,
+                              uint32_t *out, hipStream_t s);
+int64_t stream_read_dma_unit();
 // the 17..32-row instantiations (own translation unit)
 hipError_t launch_decode_rows32(const DecodeLaunch &d, hipStream_t s);
 

@@ -1274,6 +1274,25 @@ rkv_status rkv_crc32c(rkv_ctx *ctx, const void *data, uint64_t n, uint32_t *out,
   return e == hipSuccess ? RKV_OK : hip_fail(op, e);
 }
 
+rkv_status rkv_stream_read(rkv_ctx *ctx, const void *data, uint64_t bytes, int32_t mode,
+                           int32_t blocks, uint32_t *out, void *stream) {
+  const char *op = "rkv_stream_read";
+  static_assert(RKV_STREAM_DMA_UNIT == 16384, "LDS-DMA round of the stream kernel");
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (mode != 0 && mode != 1) return fail(RKV_ERR_INVALID_ARG, op, "mode=%d", mode);
+  if (blocks < 1 || blocks > (1 << 20)) return fail(RKV_ERR_INVALID_ARG, op, "blocks=%d", blocks);
+  if (!data || (mode == 0 && !out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL data/out");
+  if (reinterpret_cast<uintptr_t>(data) % 16 != 0 || bytes % 16 != 0 || bytes == 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "data/bytes (%llu) not 16-byte aligned",
+                (unsigned long long)bytes);
+  if (mode == 1 && bytes % ((uint64_t)blocks * rkv::stream_read_dma_unit()) != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "bytes %llu not a multiple of blocks * %d",
+                (unsigned long long)bytes, RKV_STREAM_DMA_UNIT);
+  hipError_t e = rkv::launch_stream_read(static_cast<const uint8_t *>(data), (int64_t)bytes, mode,
+                                         blocks, out, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
 rkv_status rkv_r4kv_header_encode(const rkv_r4kv_header *h, uint8_t out[RKV_R4KV_HEADER_BYTES]) {
   if (!h || !out) return fail(RKV_ERR_INVALID_ARG, "rkv_r4kv_header_encode", "NULL argument");
   std::memset(out, 0, RKV_R4KV_HEADER_BYTES);
