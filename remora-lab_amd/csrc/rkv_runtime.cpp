@@ -698,7 +698,7 @@ rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pa
                           const rkv_prefill_args *a, void *stream) {
   const char *op = "rkv_prefill_q8";
   if (rkv_status s = use_device(ctx, op)) return s;
-  rkv::PrefillLaunch pf;
+  rkv::PrefillLaunch pf{};
   if (rkv_status s = make_prefill(ctx, g, pages, block_tables, bt_stride, n_seqs, a, op, pf))
     return s;
   hipError_t e = rkv::launch_prefill(pf, as_stream(stream));

@@ -127,6 +127,56 @@ def test_fork_copy_on_write_pool(rkv, rko, ctx):
     pool.close()
 
 
+def test_fork_decode_pages64(rkv, rko, ctx):
+    """64-token pages, head_dim 256 (the K-in-registers decode): seq 0 holds
+    300 rows; seq 1 forks it at 256 (a page boundary) and seq 2 at 200
+    (inside page 3, copied on write); all three grow.  The decode over shared
+    and private pages equals the oracle for every sequence."""
+    torch = _torch()
+    Hkv, D, PT, Hq = 2, 256, 64, 16
+    pool = rkv.Pool(ctx, 1, Hkv, D, PT, 40, 3, 8, seed=4)
+    a = pool.alloc
+    rng = np.random.default_rng(8)
+    prompt = rng.standard_normal((300, Hkv, D)).astype(np.float32)
+    a.reserve(0, 300)
+    pool.sync_tables()
+    _append(pool, 0, 0, 0, prompt)
+    a.fork(0, 1, 256)
+    a.fork(0, 2, 200)
+    rows = {0: prompt, 1: prompt[:256], 2: prompt[:200]}
+    grow = {0: 40, 1: 100, 2: 70}
+    extra = {s: rng.standard_normal((g, Hkv, D)).astype(np.float32) for s, g in grow.items()}
+    for s, g in grow.items():
+        a.reserve(s, len(rows[s]) + g)
+    pool.sync_tables()
+    for s, g in grow.items():
+        _append(pool, 0, s, len(rows[s]), extra[s])
+        rows[s] = np.concatenate([rows[s], extra[s]])
+    ctx.sync()
+    t0, t1, t2 = (a.block_table(s) for s in range(3))
+    assert t0[:4] == t1[:4] and t0[:3] == t2[:3] and t0[3] != t2[3]
+    seqs = [0, 1, 2]
+    q = rng.standard_normal((3, 1, Hq, D)).astype(np.float32)
+    qd = torch.from_numpy(q).cuda()
+    o = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    sid = torch.tensor(seqs, dtype=torch.int32, device="cuda")
+    for part in (0, 64):
+        args = rkv.decode_args(qd, o, sid, 0.0625, 8 * PT, partition_tokens=part)
+        ws = torch.zeros(max(rkv.decode_workspace_bytes(pool.geometry, args), 4),
+                         dtype=torch.uint8, device="cuda")
+        args = rkv.decode_args(qd, o, sid, 0.0625, 8 * PT, partition_tokens=part, workspace=ws)
+        pool.decode(0, args)
+        ctx.sync()
+        got = o.cpu().numpy()
+        for i, s in enumerate(seqs):
+            enc = _encoded(rko, rows[s])
+            p = rko.fd_params(Hq, Hkv, len(rows[s]), 1024, D)
+            w = rko.rows_to_words(enc)
+            want = rko.flash_decode_reference(p, w, w, (q[i, 0] * np.float32(0.0625)).reshape(-1))
+            assert_close(got[i, 0].reshape(-1), want, what=f"partition {part} seq {s}")
+    pool.close()
+
+
 def test_copy_pages_entry_point(rkv, ctx):
     """rkv_copy_pages over 3 layer arrays with a gap between them: every pair
     copied in every layer, out-of-range pairs skipped, nothing else touched."""
