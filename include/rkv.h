@@ -138,6 +138,11 @@ rkv_status rkv_alloc_export(const rkv_alloc *a, int32_t *tables, int32_t *lens);
 rkv_status rkv_seq_fork(rkv_alloc *a, int32_t src, int32_t dst, int32_t len);
 /* Block-table entries naming `page` (0 = free). */
 rkv_status rkv_page_refs(const rkv_alloc *a, int32_t page, int32_t *refs);
+/* Times `page` has left the free list (0 = never handed out): the
+ * generation of a PhysicalPageLocation (har-kv/src/page.rs:100-105), which
+ * tells a location recorded before the page was freed and reused from a
+ * current one. */
+rkv_status rkv_page_generation(const rkv_alloc *a, int32_t page, uint64_t *gen);
 /* Move the queued copy-on-write copies, as (src, dst) page pairs, to
  * `pairs` (host, room for `cap` pairs); *n = number queued.  The copies are
  * independent of each other.  Run them (rkv_copy_pages) on the stream before
@@ -461,6 +466,96 @@ rkv_status rkv_pool_spill(rkv_pool *pool, int32_t seq, int32_t token_start, int3
 rkv_status rkv_pool_restore(rkv_pool *pool, int32_t seq, const uint8_t *page, size_t page_bytes,
                             const rkv_r4kv_expect *expect, void *staging, size_t staging_bytes,
                             int32_t *refusal, void *stream);
+
+/* ---- serving adapter ------------------------------------------------------
+ * The KV side of a BatchStepModel backend (har-serve/src/adapter.rs:28-72)
+ * as ServeScheduler::step drives it (har-serve/src/scheduler.rs:603-960):
+ * the scheduler names sequences by SequenceId (scheduler.rs:122) and each
+ * step runs prefill chunks (prefill_batch) and one-token decode rows
+ * (batch_step) as separate model calls.  The adapter owns one pool (all
+ * layers), maps live ids to pool sequences, grows them by the tokens a step
+ * consumes, and runs each layer's attention for the step's rows.  The model
+ * code around attention (projections, sampling) stays the caller's.
+ *
+ * Per step, on one stream:
+ *   rkv_serve_begin_step(prefill entries, decode entries)
+ *   for each layer: rkv_serve_prefill(...) and/or rkv_serve_decode(...)
+ *   (then rkv_serve_truncate / rkv_serve_finish as the step's outcome says;
+ *   they take effect at the next rkv_serve_begin_step). */
+typedef struct rkv_serve_desc {
+  int32_t layers;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t page_tokens;        /* the scheduler's page_size (scheduler.rs:1045-1052) */
+  int32_t num_pages;
+  int32_t max_seqs;           /* live sequences at once */
+  int32_t max_pages_per_seq;
+  int32_t q_heads;            /* multiple of kv_heads */
+  int32_t max_decode;         /* decode rows per step, 1..max_seqs */
+  int32_t max_prefill_rows;   /* prefill query rows per step, >= 0 */
+  int32_t rule;               /* RKV_Q8_CANONICAL | RKV_Q8_HARSERVE */
+  uint64_t free_list_seed;
+} rkv_serve_desc;
+
+/* One sequence in one step. */
+typedef struct rkv_serve_entry {
+  uint64_t id;       /* SequenceId */
+  int32_t tokens;    /* tokens consumed this step: 1 for a decode row, the
+                        chunk length (>= 1) for a prefill entry */
+  int32_t fork_len;  /* read at an id's first step only: > 0 starts it from the
+                        first fork_len tokens of live sequence `parent`, whose
+                        pages it shares (prefix reuse, copy-on-write) */
+  uint64_t parent;
+} rkv_serve_entry;
+
+/* Where one KV page record lives: the ExactHotQ8 representation's
+ * PhysicalPageLocation (har-kv/src/page.rs:100-115) for page `ordinal` of a
+ * sequence, i.e. tokens [ordinal*page_tokens, (ordinal+1)*page_tokens), all
+ * layers and kv heads (the KVPageId of scheduler.rs:1056-1066).  Layer l's
+ * bytes are at offset + l*layer_stride in the pool's page memory
+ * (rkv_pool_layer_pages(pool, 0)). */
+typedef struct rkv_page_location {
+  int32_t page;           /* pool page id */
+  uint64_t offset;        /* bytes from the start of a layer's page array */
+  uint64_t length;        /* page bytes of one layer (rkv_page_bytes) */
+  uint64_t layer_stride;  /* bytes between layers' page arrays */
+  uint64_t generation;    /* rkv_page_generation of the page */
+} rkv_page_location;
+
+typedef struct rkv_serve rkv_serve;
+rkv_status rkv_serve_create(rkv_ctx *ctx, const rkv_serve_desc *desc, rkv_serve **out);
+rkv_status rkv_serve_destroy(rkv_serve *s);
+rkv_pool *rkv_serve_pool(rkv_serve *s);
+/* Admit ids seen for the first time (forking those with fork_len > 0), grow
+ * every entry's sequence by its tokens and upload the tables and the step's
+ * row layout, ordered on `stream`.  An id appears at most once per step;
+ * decode entries have tokens == 1; prefill rows total <= max_prefill_rows.
+ * All-or-nothing: on RKV_ERR_OUT_OF_PAGES (or any refusal) no sequence is
+ * changed or admitted. */
+rkv_status rkv_serve_begin_step(rkv_serve *s, const rkv_serve_entry *prefill, int32_t n_prefill,
+                                const rkv_serve_entry *decode, int32_t n_decode, void *stream);
+/* One layer's attention for the step's decode rows (batch_step): q
+ * [n_decode][q_heads][head_dim], k and v [n_decode][kv_heads][head_dim] (the
+ * rows' own K/V, appended inside the decode launch), out
+ * [n_decode][q_heads][head_dim]; row b is decode entry b. */
+rkv_status rkv_serve_decode(rkv_serve *s, int32_t layer, const void *q, const void *k,
+                            const void *v, int32_t dtype, void *out, int32_t out_dtype,
+                            float scale, void *stream);
+/* One layer's attention for the step's prefill chunks (prefill_batch): rows
+ * in entry order, entry e's chunk contiguous; q [rows][q_heads][head_dim],
+ * k and v [rows][kv_heads][head_dim], out [rows][q_heads][head_dim].  Row i
+ * of a chunk that follows ctx cached tokens attends positions [0, ctx+i]. */
+rkv_status rkv_serve_prefill(rkv_serve *s, int32_t layer, const void *q, const void *k,
+                             const void *v, int32_t dtype, void *out, int32_t out_dtype,
+                             float scale, void *stream);
+/* Speculative rollback of a live id to len tokens (rkv_seq_truncate). */
+rkv_status rkv_serve_truncate(rkv_serve *s, uint64_t id, int32_t len);
+/* The id finished: its pages (those no other sequence shares) return to the
+ * free list and its pool sequence is reused. */
+rkv_status rkv_serve_finish(rkv_serve *s, uint64_t id);
+rkv_status rkv_serve_seq_len(const rkv_serve *s, uint64_t id, int32_t *len);
+rkv_status rkv_serve_page_location(const rkv_serve *s, uint64_t id, int32_t ordinal,
+                                   rkv_page_location *out);
 
 /* ---- measurement --------------------------------------------------------
  * HBM streaming-read ceiling.  No counterpart in the reference: it gives the

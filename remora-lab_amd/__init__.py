@@ -102,6 +102,24 @@ class FlashDecodeParams(C.Structure):
                 ("chunk", C.c_int32), ("head_dim", C.c_int32)]
 
 
+class ServeDesc(C.Structure):
+    _fields_ = [("layers", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("page_tokens", C.c_int32), ("num_pages", C.c_int32), ("max_seqs", C.c_int32),
+                ("max_pages_per_seq", C.c_int32), ("q_heads", C.c_int32),
+                ("max_decode", C.c_int32), ("max_prefill_rows", C.c_int32), ("rule", C.c_int32),
+                ("free_list_seed", C.c_uint64)]
+
+
+class ServeEntry(C.Structure):
+    _fields_ = [("id", C.c_uint64), ("tokens", C.c_int32), ("fork_len", C.c_int32),
+                ("parent", C.c_uint64)]
+
+
+class PageLocation(C.Structure):
+    _fields_ = [("page", C.c_int32), ("offset", C.c_uint64), ("length", C.c_uint64),
+                ("layer_stride", C.c_uint64), ("generation", C.c_uint64)]
+
+
 class PoolDesc(C.Structure):
     _fields_ = [("layers", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
                 ("page_tokens", C.c_int32), ("num_pages", C.c_int32), ("max_seqs", C.c_int32),
@@ -173,6 +191,20 @@ _SIGS = {
     "rkv_pool_restore": (C.c_int32, [P, C.c_int32, P, C.c_size_t, C.POINTER(R4kvExpect), P,
                                      C.c_size_t, I32P, P]),
     "rkv_stream_read": (C.c_int32, [P, P, C.c_uint64, C.c_int32, C.c_int32, P, P]),
+    "rkv_page_generation": (C.c_int32, [P, C.c_int32, C.POINTER(C.c_uint64)]),
+    "rkv_serve_create": (C.c_int32, [P, C.POINTER(ServeDesc), C.POINTER(P)]),
+    "rkv_serve_destroy": (C.c_int32, [P]),
+    "rkv_serve_pool": (P, [P]),
+    "rkv_serve_begin_step": (C.c_int32, [P, C.POINTER(ServeEntry), C.c_int32,
+                                         C.POINTER(ServeEntry), C.c_int32, P]),
+    "rkv_serve_decode": (C.c_int32, [P, C.c_int32, P, P, P, C.c_int32, P, C.c_int32,
+                                     C.c_float, P]),
+    "rkv_serve_prefill": (C.c_int32, [P, C.c_int32, P, P, P, C.c_int32, P, C.c_int32,
+                                      C.c_float, P]),
+    "rkv_serve_truncate": (C.c_int32, [P, C.c_uint64, C.c_int32]),
+    "rkv_serve_finish": (C.c_int32, [P, C.c_uint64]),
+    "rkv_serve_seq_len": (C.c_int32, [P, C.c_uint64, I32P]),
+    "rkv_serve_page_location": (C.c_int32, [P, C.c_uint64, C.c_int32, C.POINTER(PageLocation)]),
 }
 
 _lib = None
@@ -287,6 +319,11 @@ class Allocator:
     def fork(self, src: int, dst: int, length: int) -> None:
         """Share src's first `length` tokens with the empty sequence dst."""
         check(lib().rkv_seq_fork(self.h, src, dst, length))
+
+    def page_generation(self, page: int) -> int:
+        n = C.c_uint64()
+        check(lib().rkv_page_generation(self.h, page, C.byref(n)))
+        return n.value
 
     def page_refs(self, page: int) -> int:
         n = C.c_int32()
@@ -614,6 +651,90 @@ class Pool:
         if self.h:
             self.alloc.h = None
             lib().rkv_pool_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _entries(items):
+    """ServeEntry array from (id, tokens) or (id, tokens, fork_len, parent) tuples."""
+    arr = (ServeEntry * max(len(items), 1))()
+    for i, it in enumerate(items):
+        sid, tokens, fork_len, parent = (tuple(it) + (0, 0))[:4]
+        arr[i] = ServeEntry(sid, tokens, fork_len, parent)
+    return arr
+
+
+class Serve:
+    """Serving adapter (rkv_serve_*): one pool for all layers, sequences named
+    by the scheduler's SequenceId, per-step prefill chunks and decode rows."""
+
+    def __init__(self, ctx: Ctx, layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
+                 max_pages_per_seq, q_heads, max_decode, max_prefill_rows, rule=Q8_CANONICAL,
+                 seed=0):
+        self.ctx = ctx
+        d = ServeDesc(layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
+                      max_pages_per_seq, q_heads, max_decode, max_prefill_rows, rule, seed)
+        h = P()
+        check(lib().rkv_serve_create(ctx.h, C.byref(d), C.byref(h)))
+        self.h = h
+        self.desc = d
+        self.geometry = Geometry(kv_heads, head_dim, page_tokens, num_pages)
+        self.pool_h = P(lib().rkv_serve_pool(h))
+        self.alloc = Allocator(num_pages, page_tokens, max_seqs, max_pages_per_seq,
+                               handle=P(lib().rkv_pool_allocator(self.pool_h)))
+
+    def begin_step(self, prefill=(), decode=(), stream=None) -> None:
+        """prefill / decode: (id, tokens[, fork_len, parent]) per sequence."""
+        pe, de = _entries(list(prefill)), _entries(list(decode))
+        check(lib().rkv_serve_begin_step(self.h, pe, len(prefill), de, len(decode),
+                                         _stream(stream)))
+
+    def decode(self, layer, q, k, v, out, scale, stream=None) -> None:
+        import torch
+        check(lib().rkv_serve_decode(self.h, layer, _ptr(q), _ptr(k), _ptr(v),
+                                     BF16 if q.dtype == torch.bfloat16 else F32, _ptr(out),
+                                     BF16 if out.dtype == torch.bfloat16 else F32, scale,
+                                     _stream(stream)))
+
+    def prefill(self, layer, q, k, v, out, scale, stream=None) -> None:
+        import torch
+        check(lib().rkv_serve_prefill(self.h, layer, _ptr(q), _ptr(k), _ptr(v),
+                                      BF16 if q.dtype == torch.bfloat16 else F32, _ptr(out),
+                                      BF16 if out.dtype == torch.bfloat16 else F32, scale,
+                                      _stream(stream)))
+
+    def truncate(self, sid: int, length: int) -> None:
+        check(lib().rkv_serve_truncate(self.h, sid, length))
+
+    def finish(self, sid: int) -> None:
+        check(lib().rkv_serve_finish(self.h, sid))
+
+    def seq_len(self, sid: int) -> int:
+        n = C.c_int32()
+        check(lib().rkv_serve_seq_len(self.h, sid, C.byref(n)))
+        return n.value
+
+    def page_location(self, sid: int, ordinal: int) -> PageLocation:
+        loc = PageLocation()
+        check(lib().rkv_serve_page_location(self.h, sid, ordinal, C.byref(loc)))
+        return loc
+
+    def layer_pages(self, layer: int) -> int:
+        return lib().rkv_pool_layer_pages(self.pool_h, layer)
+
+    def gather(self, layer, sid_slot, kind, out, stream=None) -> None:
+        check(lib().rkv_pool_gather(self.pool_h, layer, sid_slot, kind, _ptr(out),
+                                    _stream(stream)))
+
+    def close(self) -> None:
+        if self.h:
+            self.alloc.h = None
+            lib().rkv_serve_destroy(self.h)
             self.h = None
 
     def __del__(self):

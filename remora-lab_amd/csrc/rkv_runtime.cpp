@@ -15,13 +15,20 @@
 
 #include "../../include/rkv.h"
 #include "rkv_crc32c.h"
+#include "rkv_host.h"
 #include "rkv_launch.h"
 
 using rkv::Geo;
+using rkv::host::fail;
+using rkv::host::hip_fail;
+using rkv::host::use_device;
 
 namespace {
-
 thread_local std::string g_last_error;
+}  // namespace
+
+namespace rkv {
+namespace host {
 
 // Mirrors HarError{operation, message} (har-vulkan/src/lib.rs:19-56): the
 // status says what kind of failure, the message says where and why.
@@ -38,6 +45,11 @@ rkv_status fail(rkv_status code, const char *op, const char *fmt, ...) {
 rkv_status hip_fail(const char *op, hipError_t e) {
   return fail(RKV_ERR_DEVICE, op, "%s (%s)", hipGetErrorString(e), hipGetErrorName(e));
 }
+
+}  // namespace host
+}  // namespace rkv
+
+namespace {
 
 uint64_t splitmix64(uint64_t x) {
   x += 0x9e3779b97f4a7c15ULL;
@@ -78,15 +90,16 @@ struct rkv_ctx {
   int32_t *d_fault = nullptr;  // device fault word (rkv::FAULT_* bits)
 };
 
-namespace {
-// Make ctx's device current for the calling thread.
+namespace rkv {
+namespace host {
 rkv_status use_device(rkv_ctx *ctx, const char *op) {
   if (!ctx) return fail(RKV_ERR_INVALID_ARG, op, "ctx is NULL");
   hipError_t e = hipSetDevice(ctx->device);
   if (e != hipSuccess) return hip_fail(op, e);
   return RKV_OK;
 }
-}  // namespace
+}  // namespace host
+}  // namespace rkv
 
 extern "C" {
 
@@ -176,6 +189,7 @@ struct rkv_alloc {
   std::vector<int32_t> held;       // pages held per sequence
   std::vector<uint8_t> dirty;      // table row changed since the last upload (lengths always go)
   std::vector<int32_t> refs;       // [num_pages] block-table entries naming the page, 0 = free
+  std::vector<uint64_t> gen;       // [num_pages] times the page left the free list
   // Copy-on-write copies queued since the last take, as (src, dst) pairs;
   // copy_src[dst] = src while the pair is queued (else -1) and copy_reads[p]
   // counts queued pairs that read p.  A page a queued pair reads is never
@@ -221,6 +235,7 @@ int32_t take_page(rkv_alloc *a) {
   const int32_t page = a->free_list.back();
   a->free_list.pop_back();
   a->refs[page] = 1;
+  ++a->gen[page];
   return page;
 }
 }  // namespace
@@ -255,6 +270,7 @@ rkv_status rkv_alloc_create(const rkv_alloc_desc *desc, rkv_alloc **out) {
   a->held.assign(desc->max_seqs, 0);
   a->dirty.assign(desc->max_seqs, 1);
   a->refs.assign(desc->num_pages, 0);
+  a->gen.assign(desc->num_pages, 0);
   a->copy_src.assign(desc->num_pages, -1);
   a->copy_reads.assign(desc->num_pages, 0);
   *out = a;
@@ -362,6 +378,15 @@ rkv_status rkv_page_refs(const rkv_alloc *a, int32_t page, int32_t *refs) {
   if (page < 0 || page >= a->d.num_pages)
     return fail(RKV_ERR_INVALID_ARG, op, "page %d outside [0, %d)", page, a->d.num_pages);
   *refs = a->refs[page];
+  return RKV_OK;
+}
+
+rkv_status rkv_page_generation(const rkv_alloc *a, int32_t page, uint64_t *gen) {
+  const char *op = "rkv_page_generation";
+  if (!a || !gen) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
+  if (page < 0 || page >= a->d.num_pages)
+    return fail(RKV_ERR_INVALID_ARG, op, "page %d outside [0, %d)", page, a->d.num_pages);
+  *gen = a->gen[page];
   return RKV_OK;
 }
 

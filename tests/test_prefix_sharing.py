@@ -203,3 +203,25 @@ def test_full_page_fork_needs_no_copy(rkv):
     assert a.take_copies() == []
     assert a.block_table(1)[:2] == a.block_table(0)[:2]
     assert a.block_table(1)[2] != a.block_table(0)[2]
+
+
+def test_page_generation_counts_reuse(rkv):
+    """A page's generation counts the times it left the free list: the pages a
+    sequence frees come back (top of the list first) one generation later,
+    and a fork shares pages without a new generation."""
+    a = rkv.Allocator(6, PT, 3, 4, seed=3)
+    assert all(a.page_generation(p) == 0 for p in range(6))
+    a.reserve(0, 3 * PT)
+    first = a.block_table(0)
+    assert [a.page_generation(p) for p in first] == [1, 1, 1]
+    a.fork(0, 1, 2 * PT)
+    assert [a.page_generation(p) for p in a.block_table(1)] == [1, 1]
+    a.free(0)
+    a.free(1)
+    a.reserve(2, 4 * PT)
+    again = a.block_table(2)
+    assert sorted(again[:3]) == sorted(first)
+    assert all(a.page_generation(p) == 2 for p in first)
+    assert a.page_generation(again[3]) == 1
+    with pytest.raises(rkv.RkvError):
+        a.page_generation(6)
