@@ -62,8 +62,10 @@ def parse():
     ap.add_argument("--config", type=int, default=1,
                     help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs; "
                          "6 = prefix-shared decode (forks + copy-on-write pages); "
-                         "7 = chunked prefill attention; 8 = R4KV page spill/restore")
+                         "7 = chunked prefill attention; 8 = R4KV page spill/restore; "
+                         "9 = serving step through the adapter")
     ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
+    ap.add_argument("--serve-layers", type=int, default=4, help="layers of config 9")
     ap.add_argument("--append-launch", action="store_true",
                     help="append the step's rows with a separate rkv_pool_append launch instead "
                          "of inside the decode launch")
@@ -915,6 +917,132 @@ def run_config7(args) -> int:
     return 0
 
 
+def run_config9(args) -> int:
+    """Serving step through the adapter (rkv_serve_*): 64 live requests with
+    lognormal contexts (median 8192, sigma 1.0, clipped to [512, 32768]) over
+    `--serve-layers` layers.  Per step: 8 rotating requests prefill a
+    512-token chunk (append + causal prefill attention) and the other 56
+    decode one token (append inside the decode launch).  Each request
+    finishes with probability 0.02 per step; its place goes to a new id that
+    starts empty or, one in four, forks the first half of a live request
+    (prefix reuse).  One begin_step per step, then prefill and decode
+    attention per layer; the value is tokens (prefill rows + decode rows)
+    through every layer's attention per second."""
+    import numpy as np
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    rng = np.random.default_rng(args.seed)
+    B, layers, Hq, Hkv, D, PT = 64, args.serve_layers, 16, 2, 256, 64
+    NPF, CH = 8, 512
+    ND = B - NPF
+    lens = np.clip(np.round(np.exp(rng.normal(math.log(8192), 1.0, B))), 512, 32768).astype(np.int64)
+    total_steps = args.warmup + args.steps
+    cap = 32768 + total_steps * CH + CH
+    pps = (cap + PT - 1) // PT
+    num_pages = int(math.ceil((int(lens.sum()) + B * total_steps * CH // 4) / PT * 1.25)) + B * 8
+    sv = rkv.Serve(ctx, layers, Hkv, D, PT, num_pages, 2 * B, pps, q_heads=Hq, max_decode=B,
+                   max_prefill_rows=NPF * CH, seed=args.seed)
+    # initial contexts: admit every id, grow it and write its rows directly
+    # (no attention for the cache fill; not timed)
+    ids = list(range(B))
+    sv.begin_step(decode=[(i, 1) for i in ids])
+    for i in ids:
+        sv.alloc.reserve(sv.slot(i), int(lens[i]))
+    sv.sync_tables()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 11)
+    sl = np.concatenate([np.full(int(L), sv.slot(i), np.int32) for i, L in zip(ids, lens)])
+    po = np.concatenate([np.arange(int(L), dtype=np.int32) for L in lens])
+    for layer in range(layers):
+        for a0 in range(0, len(sl), 1 << 16):
+            n = min(1 << 16, len(sl) - a0)
+            k = torch.randn((n, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+            v = torch.randn((n, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+            sv.pool_append(layer, torch.from_numpy(sl[a0:a0 + n]).to(dev),
+                           torch.from_numpy(po[a0:a0 + n]).to(dev), k, v)
+    ctx.sync()
+    stream = torch.cuda.current_stream()
+    qp = torch.randn((NPF * CH, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    kp = torch.randn((NPF * CH, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    vp = torch.randn((NPF * CH, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    qd = torch.randn((ND, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    kd = torch.randn((ND, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    vd = torch.randn((ND, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
+    op = torch.empty((NPF * CH, Hq, D), dtype=torch.float32, device=dev)
+    od = torch.empty((ND, Hq, D), dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    fin = np.random.default_rng(args.seed + 3)
+    cur = {i: int(lens[i]) for i in ids}
+    next_id = [B]
+    stats = {"finished": 0, "forks": 0, "decode_kv_bytes": 0, "prefill_flops": 0}
+    row = D // 32 * 34
+
+    def step(i, ev):
+        # finishes: the position's request is replaced by a new id
+        fresh = {}
+        for pos in range(B):
+            if fin.random() < 0.02:
+                sv.finish(ids[pos])
+                del cur[ids[pos]]
+                ids[pos] = next_id[0]
+                next_id[0] += 1
+                stats["finished"] += 1
+                fresh[pos] = None
+        for pos in fresh:
+            if fin.random() < 0.25 and len(cur) > 0:
+                parent = ids[(pos + 1 + int(fin.integers(B - 1))) % B]
+                if parent in cur and parent not in [ids[p] for p in fresh]:
+                    fresh[pos] = (parent, cur[parent] // 2)
+        pf_pos = [(i * NPF + j) % B for j in range(NPF)]
+        pre, dec = [], []
+        for pos in range(B):
+            sid = ids[pos]
+            n = CH if pos in pf_pos else 1
+            fk = fresh.get(pos)
+            if pos in fresh:
+                cur[sid] = fk[1] if fk else 0
+                stats["forks"] += 1 if fk else 0
+            e = (sid, n, fk[1], fk[0]) if fk else (sid, n)
+            (pre if n > 1 else dec).append(e)
+            if n == 1:
+                stats["decode_kv_bytes"] += layers * (cur[sid] + 1) * Hkv * 2 * row
+            else:
+                stats["prefill_flops"] += layers * 4 * D * Hq * sum(cur[sid] + j + 1 for j in range(n))
+            cur[sid] += n
+        sv.begin_step(prefill=pre, decode=dec, stream=stream)
+        for layer in range(layers):
+            sv.prefill(layer, qp, kp, vp, op, scale, stream=stream)
+            sv.decode(layer, qd, kd, vd, od, scale, stream=stream)
+
+    wall, _ = _time_steps(args, stream, step)
+    ctx.sync()
+    tokens = NPF * CH + ND
+    res = {
+        "metric": "config 9: serving step through the adapter, tokens through attention per second",
+        "value": round(tokens / wall, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 QK + f16 PV, f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0; bf16 q)",
+        "config": {"workload": f"config 9 serving step (rkv_serve_*): 64 requests, lognormal "
+                               f"contexts (median 8192, sigma 1.0, [512, 32768]); per step 8 x "
+                               f"{CH}-token prefill chunks + {ND} decode rows, {layers} layers, "
+                               f"2% finish per step, 1 in 4 new requests fork a live prefix",
+                   "layers": layers, "pool_pages": num_pages},
+        "us_per_step": round(wall * 1e6, 2),
+        "us_per_layer_step": round(wall * 1e6 / layers, 2),
+        "finished_total": stats["finished"], "forks_total": stats["forks"],
+        "mean_decode_kv_gb_per_step": round(stats["decode_kv_bytes"] / total_steps / 1e9, 4),
+        "mean_prefill_tflop_per_step": round(stats["prefill_flops"] / total_steps / 1e12, 4),
+    }
+    print(json.dumps(res), flush=True)
+    sv.close()
+    ctx.close()
+    return 0
+
+
 def run_config8(args) -> int:
     """Off-HBM tier (R4KV pages): a 4096-token range of one sequence over 48
     layers (Hkv=2, D=256, page 64) is one page of 214 MB.  Timed, with HIP
@@ -1005,6 +1133,8 @@ if __name__ == "__main__":
         sys.exit(run_config4(_a))
     if _a.config == 6:
         sys.exit(run_config6(_a))
+    if _a.config == 9:
+        sys.exit(run_config9(_a))
     if _a.config in (2, 3, 5):
         sys.exit(run_config(_a))
     sys.exit(main())

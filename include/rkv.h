@@ -554,6 +554,9 @@ rkv_status rkv_serve_truncate(rkv_serve *s, uint64_t id, int32_t len);
  * free list and its pool sequence is reused. */
 rkv_status rkv_serve_finish(rkv_serve *s, uint64_t id);
 rkv_status rkv_serve_seq_len(const rkv_serve *s, uint64_t id, int32_t *len);
+/* The pool sequence of a live id, for pool-level calls on it: rkv_pool_spill
+ * / rkv_pool_restore (off-HBM tier), rkv_pool_gather, rkv_pool_append. */
+rkv_status rkv_serve_seq_slot(const rkv_serve *s, uint64_t id, int32_t *slot);
 rkv_status rkv_serve_page_location(const rkv_serve *s, uint64_t id, int32_t ordinal,
                                    rkv_page_location *out);
 

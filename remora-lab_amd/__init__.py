@@ -205,6 +205,7 @@ _SIGS = {
     "rkv_serve_finish": (C.c_int32, [P, C.c_uint64]),
     "rkv_serve_seq_len": (C.c_int32, [P, C.c_uint64, I32P]),
     "rkv_serve_page_location": (C.c_int32, [P, C.c_uint64, C.c_int32, C.POINTER(PageLocation)]),
+    "rkv_serve_seq_slot": (C.c_int32, [P, C.c_uint64, I32P]),
 }
 
 _lib = None
@@ -718,6 +719,22 @@ class Serve:
         n = C.c_int32()
         check(lib().rkv_serve_seq_len(self.h, sid, C.byref(n)))
         return n.value
+
+    def slot(self, sid: int) -> int:
+        """The pool sequence of a live id (for pool-level calls on it)."""
+        n = C.c_int32()
+        check(lib().rkv_serve_seq_slot(self.h, sid, C.byref(n)))
+        return n.value
+
+    def pool_append(self, layer, slots, positions, k, v, stream=None) -> None:
+        """rkv_pool_append on the adapter's pool: rows of pool sequences `slots`."""
+        import torch
+        a = AppendArgs(slots.numel(), _ptr(slots), _ptr(positions), _ptr(k), _ptr(v),
+                       BF16 if k.dtype == torch.bfloat16 else F32, Q8_CANONICAL)
+        check(lib().rkv_pool_append(self.pool_h, layer, C.byref(a), _stream(stream)))
+
+    def sync_tables(self, stream=None) -> None:
+        check(lib().rkv_pool_sync_tables(self.pool_h, _stream(stream)))
 
     def page_location(self, sid: int, ordinal: int) -> PageLocation:
         loc = PageLocation()

@@ -351,6 +351,11 @@ rkv_status rkv_serve_seq_len(const rkv_serve *s, uint64_t id, int32_t *len) {
   return rkv_seq_len(rkv_pool_allocator(s->pool), slot, len);
 }
 
+rkv_status rkv_serve_seq_slot(const rkv_serve *s, uint64_t id, int32_t *slot) {
+  if (!slot) return fail(RKV_ERR_INVALID_ARG, "rkv_serve_seq_slot", "slot is NULL");
+  return live_slot(s, id, "rkv_serve_seq_slot", slot);
+}
+
 rkv_status rkv_serve_page_location(const rkv_serve *s, uint64_t id, int32_t ordinal,
                                    rkv_page_location *out) {
   const char *op = "rkv_serve_page_location";
