@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 def _shape(seed):
     rng = np.random.default_rng(1000 + seed)
     D = int(rng.choice([128, 256]))
-    PT = int(rng.choice([16, 32, 64, 128]))
+    PT = int(rng.choice([16, 32, 64, 128, 256]))
     Hkv = int(rng.choice([1, 2, 4]))
     G = int(rng.choice([1, 2, 4, 8]))
     q_len = int(rng.choice([1, 1, 2, 4]))
@@ -33,7 +33,7 @@ def _shape(seed):
                 q_bf16=bool(rng.random() < 0.5), outliers=0.01 if rng.random() < 0.3 else 0.0)
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(24))
 def test_random_decode_shapes(rkv, rko, ctx, seed):
     c = _shape(seed)
     print(f"seed {seed}: {c}", flush=True)
@@ -56,7 +56,7 @@ def test_random_prefill_shapes(rkv, rko, ctx, seed):
     torch = __import__("torch")
     rng = np.random.default_rng(2000 + seed)
     D = int(rng.choice([128, 256]))
-    PT = int(rng.choice([16, 32, 64, 128]))
+    PT = int(rng.choice([16, 32, 64, 128, 256]))
     Hkv = int(rng.choice([1, 2]))
     G = int(rng.choice([1, 2, 4, 8, 16]))
     Hq = Hkv * G
