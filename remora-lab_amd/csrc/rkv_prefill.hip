@@ -31,11 +31,13 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillL
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
-  // entry of this row block (the table is in the kernel arguments)
+  // entry of this row block (the table is in the kernel arguments); an
+  // entry's row blocks are taken last block first (longest causal range
+  // first, as the entries themselves are ordered)
   const int32_t x = (int32_t)blockIdx.x;
   int e = 0;
   while (e + 1 < pf.n_entries && x >= pf.first[e + 1]) ++e;
-  const int32_t rb = x - pf.first[e];
+  const int32_t rb = pf.first[e + 1] - 1 - x;
   const int32_t seq = pf.seq[e], ctx = pf.ctx[e], n = pf.rows[e];
   const int32_t j0 = pf.tq * rb;
   const int32_t jn = min(pf.tq, n - j0);

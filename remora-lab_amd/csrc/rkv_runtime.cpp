@@ -674,8 +674,19 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   pf = rkv::PrefillLaunch{};
   pf.tq = rkv::kPrefillRows / G;
   pf.n_entries = a->n_seqs;
+  // Longest first: a row block's time grows with its causal range, so the
+  // entries go into the launch table by descending ctx + rows (and the
+  // kernel takes each entry's later row blocks first), which keeps a long
+  // entry dispatched last from setting the launch's end.  Outputs are
+  // addressed per entry, so the order changes nothing else.
+  int32_t order[RKV_PREFILL_MAX_SEQS];
+  for (int32_t e = 0; e < a->n_seqs; ++e) order[e] = e;
+  std::stable_sort(order, order + a->n_seqs, [&](int32_t x, int32_t y) {
+    return (int64_t)a->ctx_lens[x] + a->q_rows[x] > (int64_t)a->ctx_lens[y] + a->q_rows[y];
+  });
   int64_t blocks = 0;
-  for (int32_t e = 0; e < a->n_seqs; ++e) {
+  for (int32_t k = 0; k < a->n_seqs; ++k) {
+    const int32_t e = order[k];
     const int32_t seq = a->seq_ids[e], c = a->ctx_lens[e], n = a->q_rows[e], off = a->q_offsets[e];
     if (seq < 0 || seq >= n_seqs)
       return fail(RKV_ERR_INVALID_ARG, op, "entry %d: seq %d outside [0, %d)", e, seq, n_seqs);
@@ -687,11 +698,11 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
         (end + g->page_tokens - 1) / g->page_tokens > rkv::kPrefillMaxPages)
       return fail(RKV_ERR_UNSUPPORTED, op, "entry %d: %lld tokens exceed the table row (%d pages, "
                   "at most %d)", e, (long long)end, bt_stride, rkv::kPrefillMaxPages);
-    pf.seq[e] = seq;
-    pf.ctx[e] = c;
-    pf.rows[e] = n;
-    pf.qoff[e] = off;
-    pf.first[e] = (int32_t)blocks;
+    pf.seq[k] = seq;
+    pf.ctx[k] = c;
+    pf.rows[k] = n;
+    pf.qoff[k] = off;
+    pf.first[k] = (int32_t)blocks;
     blocks += (n + pf.tq - 1) / pf.tq;
   }
   pf.first[a->n_seqs] = (int32_t)blocks;
