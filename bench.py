@@ -66,6 +66,12 @@ def parse():
                          "9 = serving step through the adapter")
     ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
     ap.add_argument("--serve-layers", type=int, default=4, help="layers of config 9")
+    ap.add_argument("--prefill-batch", type=int, default=8, help="sequences of config 7")
+    ap.add_argument("--prefill-ctx", type=int, default=8192, help="cached tokens of config 7")
+    ap.add_argument("--prefill-rows", type=int, default=512, help="chunk rows of config 7")
+    ap.add_argument("--prefill-segment", type=int, default=0,
+                    help="config 7 segment_tokens: 0 = automatic split (with a workspace), "
+                         "> 0 = that segment length, -1 = never split")
     ap.add_argument("--append-launch", action="store_true",
                     help="append the step's rows with a separate rkv_pool_append launch instead "
                          "of inside the decode launch")
@@ -846,7 +852,10 @@ def run_config7(args) -> int:
     prefill attention over them (rkv_pool_prefill), rotating over 4 layer
     pools.  Rows of a chunk attend causally: row i sees ctx + i + 1 tokens.
     `value` is attention TFLOP/s, 4*D flops per (query row, visible token),
-    against the dense f16 MFMA peak; the prefill kernel is HIP-event timed."""
+    against the dense f16 MFMA peak; the prefill kernel (and the split's
+    combine, when the launch splits) is HIP-event timed.  --prefill-batch,
+    --prefill-ctx and --prefill-rows change the shape (one long-context chunk
+    leaves most workgroup slots idle unless its causal ranges are split)."""
     import numpy as np
     import torch
     rkv = load_rkv()
@@ -854,7 +863,7 @@ def run_config7(args) -> int:
     torch.cuda.set_device(dev)
     ctx = rkv.Ctx(0)
     Hq, Hkv, D, PT = 16, 2, 256, 64
-    B, layers, C0, N = 8, 4, 8192, 512
+    B, layers, C0, N = args.prefill_batch, 4, args.prefill_ctx, args.prefill_rows
     L = C0 + N
     pps = (L + PT - 1) // PT
     num_pages = int(math.ceil(B * pps * 1.10))
@@ -874,7 +883,11 @@ def run_config7(args) -> int:
     v_new = torch.randn((rows, Hkv, D), generator=gen, device=dev).to(torch.bfloat16)
     q = torch.randn((rows, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
     out = torch.empty((rows, Hq, D), device=dev, dtype=torch.float32)
-    pa = rkv.prefill_args(list(range(B)), [C0] * B, [N] * B, q, out, 1.0 / math.sqrt(D))
+    ent = (list(range(B)), [C0] * B, [N] * B, q, out, 1.0 / math.sqrt(D))
+    ws_bytes = rkv.prefill_workspace_bytes(
+        pool.geometry, rkv.prefill_args(*ent, segment_tokens=args.prefill_segment))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    pa = rkv.prefill_args(*ent, segment_tokens=args.prefill_segment, workspace=ws)
     stream = torch.cuda.current_stream()
 
     def step(i, ev):
@@ -902,7 +915,8 @@ def run_config7(args) -> int:
         "config": {"workload": (f"chunked prefill: B={B} sequences, ctx={C0} cached + {N}-row chunk "
                                 f"each (causal), Hq=16, Hkv=2, D=256, page 64, append + attention "
                                 f"per step, {layers} rotating layer pools"),
-                   "batch": B, "ctx": C0, "chunk_rows": N, "layers_rotated": layers},
+                   "batch": B, "ctx": C0, "chunk_rows": N, "layers_rotated": layers,
+                   "segment_tokens": args.prefill_segment, "split_workspace_bytes": ws_bytes},
         "us_per_step": round(wall * 1e6, 2),
         "flops_per_step": flops,
         "roofline": {"bound": "mfma", "kernel": "rkv::prefill_kernel<256, false, 2>",

@@ -218,6 +218,15 @@ typedef struct rkv_prefill_args {
   float scale;              /* softmax scale on q.k */
   void *out;                /* device [total_rows][q_heads][head_dim] */
   int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
+  /* Split-K over the causal range (a row block's range in segments, merged
+   * by the decode's log-sum-exp combine).  0: split when the launch has
+   * fewer row blocks than the device has workgroup slots and `workspace`
+   * holds the partials; > 0: segments of this many tokens (rounded up to a
+   * multiple of max(32, page_tokens), and to at most 64 segments); < 0:
+   * never split. */
+  int32_t segment_tokens;
+  void *workspace;          /* device, 256-byte aligned, or NULL (no split) */
+  size_t workspace_bytes;
 } rkv_prefill_args;
 
 /* ---- kernel-level entry points (explicit device pointers) -----------------
@@ -272,10 +281,15 @@ rkv_status rkv_splitk_combine(rkv_ctx *ctx, const float *ml, const float *o,
 
 /* Chunked prefill attention over the pages (see rkv_prefill_args); rows of
  * entries whose range exceeds the block-table row (or 4096 pages) are
- * refused with RKV_ERR_UNSUPPORTED. */
+ * refused with RKV_ERR_UNSUPPORTED.  An explicit segment_tokens whose
+ * partials do not fit workspace_bytes is refused with RKV_ERR_INVALID_ARG. */
 rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                           const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
                           const rkv_prefill_args *args, void *stream);
+/* Workspace bytes the split of these arguments uses: with segment_tokens > 0
+ * that split, with 0 the split chosen when the workspace is large enough
+ * (0 when none is); the device pointers in args are not read. */
+size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_args *args);
 
 /* Export seq's K or V cache in the reference contiguous layout
  * [kv_heads][len][head_dim/32*34] bytes (what flash_decode_reference reads,

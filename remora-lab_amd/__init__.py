@@ -76,7 +76,8 @@ class DecodeArgs(C.Structure):
 class PrefillArgs(C.Structure):
     _fields_ = [("n_seqs", C.c_int32), ("seq_ids", I32P), ("ctx_lens", I32P), ("q_rows", I32P),
                 ("q_offsets", I32P), ("total_rows", C.c_int32), ("q", P), ("q_dtype", C.c_int32),
-                ("q_heads", C.c_int32), ("scale", C.c_float), ("out", P), ("out_dtype", C.c_int32)]
+                ("q_heads", C.c_int32), ("scale", C.c_float), ("out", P), ("out_dtype", C.c_int32),
+                ("segment_tokens", C.c_int32), ("workspace", P), ("workspace_bytes", C.c_size_t)]
 
 
 PREFILL_MAX_SEQS = 64
@@ -154,6 +155,7 @@ _SIGS = {
     "rkv_decode_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P, C.c_int32,
                                   C.POINTER(DecodeArgs), P]),
     "rkv_decode_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
+    "rkv_prefill_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(PrefillArgs)]),
     "rkv_decode_partition_tokens": (C.c_int32, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
     "rkv_decode_q8_partials": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P,
                                            C.c_int32, C.POINTER(DecodeArgs), P, P, P]),
@@ -416,9 +418,12 @@ def decode_args(q, out, seq_ids, scale, max_seq_len, q_len=1, partition_tokens=0
     return a
 
 
-def prefill_args(seq_ids, ctx_lens, q_rows, q, out, scale, q_offsets=None) -> PrefillArgs:
+def prefill_args(seq_ids, ctx_lens, q_rows, q, out, scale, q_offsets=None, segment_tokens=0,
+                 workspace=None) -> PrefillArgs:
     """Host entry table (lists of ints) + device q/out [total_rows][q_heads][D].
-    q_offsets defaults to the running sum of q_rows."""
+    q_offsets defaults to the running sum of q_rows.  segment_tokens and the
+    device tensor `workspace` control the split of row blocks' causal ranges
+    (0 with a workspace: automatic; > 0: that segment length; < 0: never)."""
     import torch
     n = len(seq_ids)
     if q_offsets is None:
@@ -429,9 +434,15 @@ def prefill_args(seq_ids, ctx_lens, q_rows, q, out, scale, q_offsets=None) -> Pr
     arr = [(C.c_int32 * max(n, 1))(*[int(v) for v in x]) for x in (seq_ids, ctx_lens, q_rows, q_offsets)]
     a = PrefillArgs(n, *[C.cast(x, I32P) for x in arr], q.shape[0], _ptr(q),
                     BF16 if q.dtype == torch.bfloat16 else F32, q.shape[1], scale, _ptr(out),
-                    BF16 if out.dtype == torch.bfloat16 else F32)
-    a._refs = (q, out, arr)  # the struct holds raw pointers
+                    BF16 if out.dtype == torch.bfloat16 else F32, int(segment_tokens),
+                    _ptr(workspace) if workspace is not None else None,
+                    workspace.numel() * workspace.element_size() if workspace is not None else 0)
+    a._refs = (q, out, arr, workspace)  # the struct holds raw pointers
     return a
+
+
+def prefill_workspace_bytes(g: Geometry, a: PrefillArgs) -> int:
+    return lib().rkv_prefill_workspace_bytes(C.byref(g), C.byref(a))
 
 
 def prefill_q8(ctx: Ctx, g: Geometry, pages, block_tables, n_seqs: int, a: PrefillArgs,

@@ -95,13 +95,21 @@ hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s);
 // Chunked prefill attention: entry e holds rows[e] query rows of sequence
 // seq[e] at positions ctx[e] .. ctx[e]+rows[e]-1 (already appended), stored
 // at rows qoff[e].. of q/out ([rows][q_heads][head_dim]); row i attends
-// positions [0, ctx[e]+i].  Workgroup x of the grid (first[n_entries],
-// kv_heads) takes row block x - first[e] of the entry with first[e] <= x <
-// first[e+1]: tq query tokens x q_heads/kv_heads heads = kPrefillRows rows.
+// positions [0, ctx[e]+i].  A row block is tq query tokens x
+// q_heads/kv_heads heads = kPrefillRows rows; its causal range is split into
+// nseg[e] segments of seg[e] tokens.  Workgroup x of the grid
+// (first[n_entries], kv_heads) takes unit u = first[e+1] - 1 - x of the
+// entry with first[e] <= x < first[e+1]: row block u / nseg[e], segment
+// u % nseg[e].  An entry with one segment writes its rows normalized; a
+// split one writes per-segment partials (m, l) and o at partial row
+// wsoff[e] + (row * q_heads + head) * nseg[e] + segment, which
+// launch_prefill's combine merges into the rows.
 constexpr int kPrefillWaves = 8;
 constexpr int kPrefillRows = 16 * kPrefillWaves;
 constexpr int kPrefillMaxEntries = 64;
-constexpr int kPrefillMaxPages = 4096;  // page-list capacity of one row block (LDS)
+constexpr int kPrefillMaxPages = 4096;  // page-list capacity of one unit (LDS)
+constexpr int kPrefillMaxSegs = 64;
+constexpr int kPrefillWgsPerCu = 2;  // the prefill kernel's launch bounds
 struct PrefillLaunch {
   DecodeLaunch d;  // geometry, pages, tables, q, out, dtypes, scale, fault, stages
   int32_t tq;
@@ -110,7 +118,12 @@ struct PrefillLaunch {
   int32_t ctx[kPrefillMaxEntries];
   int32_t rows[kPrefillMaxEntries];
   int32_t qoff[kPrefillMaxEntries];
+  int32_t nseg[kPrefillMaxEntries];
+  int32_t seg[kPrefillMaxEntries];     // tokens, a multiple of max(32, page_tokens)
+  int64_t wsoff[kPrefillMaxEntries];   // first partial row of a split entry
   int32_t first[kPrefillMaxEntries + 1];
+  float *ws_ml;  // split partials: (m, l) [partial row][2] ...
+  float *ws_o;   // ... and o [partial row][head_dim]
 };
 hipError_t launch_prefill(const PrefillLaunch &pf, hipStream_t s);
 

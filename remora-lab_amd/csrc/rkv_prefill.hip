@@ -12,16 +12,19 @@
 // softmax, f16 PV MFMA) is the decode kernel's, with the causal limit of
 // every row at ctx + its token + 1; the V codes of each tile are widened to
 // f16 once per workgroup (each wave its share) instead of once per wave.
-// The block walks its whole causal range [0, ctx + last token of the
-// block], with the range's page ids staged in an LDS list.  Output rows are
-// written normalized; no workspace.
+// A block walks its causal range [0, ctx + last token of the block] in one
+// workgroup, or, when the launch has too few blocks to fill the chip, in
+// nseg workgroups that take a segment each and write unnormalized partials
+// (m, l, o) to a workspace; a combine kernel then merges the segments of
+// each row (the decode's split-K and LSE merge, here across a block's rows).
+// The unit's page ids are staged in an LDS list.
 #include "rkv_decode_kernel.h"
 
 namespace rkv {
 namespace {
 
 template <int D, bool kSmall, int NS>
-__global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillLaunch pf) {
+__global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_kernel(PrefillLaunch pf) {
 #if defined(__HIP_DEVICE_COMPILE__)
   using Dec = Decoder<D, 2, kSmall, NS, kPrefillWaves, true, true>;
   using S = StageShape<D>;
@@ -31,13 +34,15 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillL
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
-  // entry of this row block (the table is in the kernel arguments); an
-  // entry's row blocks are taken last block first (longest causal range
+  // entry and unit of this workgroup (the table is in the kernel
+  // arguments); an entry's units are taken last first (longest causal range
   // first, as the entries themselves are ordered)
   const int32_t x = (int32_t)blockIdx.x;
   int e = 0;
   while (e + 1 < pf.n_entries && x >= pf.first[e + 1]) ++e;
-  const int32_t rb = pf.first[e + 1] - 1 - x;
+  const int32_t u = pf.first[e + 1] - 1 - x;
+  const int32_t ns = pf.nseg[e];
+  const int32_t rb = u / ns, sg = u % ns;
   const int32_t seq = pf.seq[e], ctx = pf.ctx[e], n = pf.rows[e];
   const int32_t j0 = pf.tq * rb;
   const int32_t jn = min(pf.tq, n - j0);
@@ -46,15 +51,26 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillL
     if (threadIdx.x == 0) atomicOr(p.fault, FAULT_BAD_SEQ);
     return;
   }
-  const int32_t npg = (len + g.page_tokens - 1) / g.page_tokens;
-  if (len > p.bt_stride * g.page_tokens || npg > kPrefillMaxPages) {
+  if (len > p.bt_stride * g.page_tokens) {
     if (threadIdx.x == 0) atomicOr(p.fault, FAULT_BAD_POSITION);
     return;
   }
-  // the block's page ids; bad entries are reported and replaced by page 0 so
+  // this unit's part of the causal range, tokens [tok0, tok_end): the whole
+  // range, or segment sg (empty past the block's extent; seg is a multiple
+  // of the tile and of the page, so every tile but the range's last is whole
+  // and lies in the unit's pages)
+  const int32_t tok0 = min(sg * pf.seg[e], len);
+  const int32_t tok_end = ns == 1 ? len : min(len, tok0 + pf.seg[e]);
+  const int32_t pg0 = tok0 / g.page_tokens;
+  const int32_t npg = tok_end > tok0 ? (tok_end - 1) / g.page_tokens - pg0 + 1 : 0;
+  if (npg > kPrefillMaxPages) {
+    if (threadIdx.x == 0) atomicOr(p.fault, FAULT_BAD_POSITION);
+    return;
+  }
+  // the unit's page ids; bad entries are reported and replaced by page 0 so
   // every copy stays inside the pool
   for (int32_t i = threadIdx.x; i < npg; i += 64 * kPrefillWaves) {
-    int32_t pid = p.bt[(int64_t)seq * p.bt_stride + i];
+    int32_t pid = p.bt[(int64_t)seq * p.bt_stride + pg0 + i];
     if (pid < 0 || pid >= g.num_pages) {
       atomicOr(p.fault, FAULT_BAD_PAGE);
       pid = 0;
@@ -75,11 +91,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillL
   dc.b = e;
   dc.seq = seq;
   dc.len = len;
-  dc.tok0 = 0;
-  dc.tok_end = len;
-  dc.n_tiles = (len + kTile - 1) / kTile;
+  dc.tok0 = tok0;
+  dc.tok_end = tok_end;
+  dc.n_tiles = (tok_end - tok0 + kTile - 1) / kTile;
   dc.app_mode = 0;
-  dc.pg_first = 0;
+  dc.pg_first = pg0;
   dc.pidv = 0;
   dc.pg_lds = (const __attribute__((address_space(3))) int32_t *)page_list;
   dc.vf16 = (lds_u8 *)v_f16;
@@ -119,10 +135,75 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void prefill_kernel(PrefillL
   const int r = r0 + li;
   const int jl = r / G;
   if (jl < jn) {
-    const int64_t orow = (int64_t)(pf.qoff[e] + j0 + jl) * p.q_heads + kvh * G + r % G;
-    store_out_row<D>(p.out, p.out_bf16 != 0, orow, dc.oacc[0], l, lg);
+    const int64_t erow = (int64_t)(j0 + jl) * p.q_heads + kvh * G + r % G;  // row within the entry
+    if (ns == 1) {
+      store_out_row<D>(p.out, p.out_bf16 != 0, (int64_t)pf.qoff[e] * p.q_heads + erow,
+                       dc.oacc[0], l, lg);
+    } else {
+      const int64_t prow = pf.wsoff[e] + erow * ns + sg;
+#pragma unroll
+      for (int m = 0; m < D / 16; ++m)
+        *reinterpret_cast<v4f *>(pf.ws_o + prow * D + 16 * m + 4 * lg) = dc.oacc[0][m];
+      if (lg == 0) *reinterpret_cast<float2 *>(pf.ws_ml + 2 * prow) = float2{dc.mref[0], l};
+    }
   }
 #endif  // __HIP_DEVICE_COMPILE__
+}
+
+// Rows of the split entries, one workgroup of 64 threads each, four
+// dimensions a thread: merge the row's nseg partials in base 2 (M = max m,
+// L = sum l 2^(m-M), O = sum o 2^(m-M)) and write O / L (0 when L is 0).
+// Workgroup x takes row x - cfirst[k] of split entry k, cfirst[k] <= x <
+// cfirst[k+1].
+struct PrefillCombine {
+  int32_t n_entries;
+  int32_t q_heads;
+  int32_t out_bf16;
+  void *out;
+  const float *ml, *o;
+  int32_t cfirst[kPrefillMaxEntries + 1];  // rows * q_heads of the split entries, cumulative
+  int32_t qoff[kPrefillMaxEntries];
+  int32_t nseg[kPrefillMaxEntries];
+  int64_t wsoff[kPrefillMaxEntries];
+};
+
+template <int D>
+__global__ __launch_bounds__(64) void prefill_combine_kernel(PrefillCombine c) {
+  const int32_t x = (int32_t)blockIdx.x;
+  int e = 0;
+  while (e + 1 < c.n_entries && x >= c.cfirst[e + 1]) ++e;
+  const int32_t erow = x - c.cfirst[e];  // token * q_heads + head within the entry
+  const int dt = threadIdx.x;
+  if (dt >= D / 4) return;
+  const int32_t ns = c.nseg[e];
+  const int64_t p0 = c.wsoff[e] + (int64_t)erow * ns;
+  float M = -INFINITY;
+  for (int32_t s = 0; s < ns; ++s) M = fmaxf(M, c.ml[2 * (p0 + s)]);
+  float L = 0.0f;
+  float o4[4] = {0.f, 0.f, 0.f, 0.f};
+  if (M != -INFINITY) {
+    for (int32_t s = 0; s < ns; ++s) {
+      const float2 ml = *reinterpret_cast<const float2 *>(c.ml + 2 * (p0 + s));
+      if (ml.x == -INFINITY) continue;
+      const float w = __builtin_amdgcn_exp2f(ml.x - M);
+      const v4f o = *reinterpret_cast<const v4f *>(c.o + (p0 + s) * D + 4 * dt);
+      L += ml.y * w;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o4[i] += o[i] * w;
+    }
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  const int64_t oi = ((int64_t)c.qoff[e] * c.q_heads + erow) * D + 4 * dt;
+  if (c.out_bf16) {
+    const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(o4[0] * inv) |
+                        ((uint32_t)f32_to_bf16_rtne(o4[1] * inv) << 16);
+    const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(o4[2] * inv) |
+                        ((uint32_t)f32_to_bf16_rtne(o4[3] * inv) << 16);
+    *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(c.out) + oi) = uint2{w0, w1};
+  } else {
+    *reinterpret_cast<v4f *>(static_cast<float *>(c.out) + oi) =
+        v4f{o4[0] * inv, o4[1] * inv, o4[2] * inv, o4[3] * inv};
+  }
 }
 
 template <int D, int NS>
@@ -132,6 +213,28 @@ hipError_t launch_prefill_t(const PrefillLaunch &pf, hipStream_t s) {
     hipLaunchKernelGGL((prefill_kernel<D, true, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
   else
     hipLaunchKernelGGL((prefill_kernel<D, false, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  // merge the split entries' partials into their rows
+  PrefillCombine c{};
+  c.q_heads = pf.d.q_heads;
+  c.out_bf16 = pf.d.out_bf16;
+  c.out = pf.d.out;
+  c.ml = pf.ws_ml;
+  c.o = pf.ws_o;
+  int32_t rows = 0;
+  for (int32_t i = 0; i < pf.n_entries; ++i) {
+    if (pf.nseg[i] < 2) continue;
+    c.cfirst[c.n_entries] = rows;
+    c.qoff[c.n_entries] = pf.qoff[i];
+    c.nseg[c.n_entries] = pf.nseg[i];
+    c.wsoff[c.n_entries] = pf.wsoff[i];
+    rows += pf.rows[i] * pf.d.q_heads;
+    ++c.n_entries;
+  }
+  c.cfirst[c.n_entries] = rows;
+  if (rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(prefill_combine_kernel<D>, dim3((unsigned)rows), dim3(64), 0, s, c);
   return hipGetLastError();
 }
 

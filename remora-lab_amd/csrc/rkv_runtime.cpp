@@ -645,8 +645,87 @@ rkv_status check_tables(const void *pages, const int32_t *bt, int32_t bt_stride,
   return RKV_OK;
 }
 
+// Split-K plan of a prefill launch: segment length in tokens (0: no split)
+// and the partial rows it writes, rows * q_heads * nseg summed over the
+// entries with more than one segment.  An entry's segment count follows its
+// longest row block (the last), ctx + rows tokens.
+struct SegPlan {
+  int32_t seg = 0;
+  int64_t partial_rows = 0;
+};
+
+constexpr int32_t kPrefillMinSegment = 1024;  // tokens: 32 tiles a unit at least
+
+int32_t segments_of(int64_t range, int32_t seg) {
+  return seg > 0 && range > seg ? (int32_t)((range + seg - 1) / seg) : 1;
+}
+
+size_t prefill_ws_bytes(int64_t partial_rows, int32_t head_dim) {
+  if (partial_rows <= 0) return 0;
+  const size_t ml = ((size_t)partial_rows * 8 + 255) / 256 * 256;
+  return ml + (size_t)partial_rows * head_dim * 4;
+}
+
+// cap: workspace bytes available to the automatic split.
+SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int32_t n,
+                      const int32_t *ctx_lens, const int32_t *q_rows, int32_t request,
+                      size_t cap) {
+  SegPlan none;
+  if (request < 0 || n <= 0) return none;
+  const int64_t unit = std::max<int32_t>(32, g->page_tokens);
+  auto round_up = [&](int64_t t) { return (t + unit - 1) / unit * unit; };
+  int64_t max_range = 0, blocks = 0;
+  for (int32_t e = 0; e < n; ++e) {
+    max_range = std::max<int64_t>(max_range, (int64_t)ctx_lens[e] + q_rows[e]);
+    blocks += ((int64_t)q_rows[e] + tq - 1) / tq;
+  }
+  auto rows_for = [&](int64_t seg) {
+    int64_t p = 0;
+    for (int32_t e = 0; e < n; ++e) {
+      const int32_t ns = segments_of((int64_t)ctx_lens[e] + q_rows[e], (int32_t)seg);
+      if (ns > 1) p += (int64_t)q_rows[e] * q_heads * ns;
+    }
+    return p;
+  };
+  const int64_t seg_floor = round_up((max_range + rkv::kPrefillMaxSegs - 1) / rkv::kPrefillMaxSegs);
+  if (request > 0) {
+    SegPlan pl;
+    pl.seg = (int32_t)std::min<int64_t>(std::max(round_up(request), seg_floor), INT32_MAX);
+    pl.partial_rows = rows_for(pl.seg);
+    if (pl.partial_rows == 0) pl.seg = 0;
+    return pl;
+  }
+  // automatic: only a launch with fewer row blocks than compute units.  One
+  // prefill workgroup keeps a CU about as busy as two, so a CU's time is the
+  // sum of its units: k equal segments a block take ceil(units*k/CUs)/k of
+  // the unsplit time.  The fewest segments reaching the least of that, when
+  // it saves a tenth at least.
+  const int64_t units = blocks * g->kv_heads;
+  const int64_t cus = rkv::kComputeUnits;
+  if (units <= 0 || units >= cus) return none;
+  const int64_t k_max = std::min<int64_t>(rkv::kPrefillMaxSegs, max_range / kPrefillMinSegment);
+  auto cost = [&](int64_t k) { return (double)((units * k + cus - 1) / cus) / (double)k; };
+  double least = 1.0;
+  for (int64_t k = 2; k <= k_max; ++k) least = std::min(least, cost(k));
+  if (least > 0.9) return none;
+  int64_t want = 2;
+  while (cost(want) > least * 1.0001) ++want;
+  int64_t seg = std::max<int64_t>({round_up((max_range + want - 1) / want),
+                                   round_up(kPrefillMinSegment), seg_floor});
+  for (; seg < max_range; seg *= 2) {
+    const int64_t p = rows_for(seg);
+    if (p > 0 && prefill_ws_bytes(p, g->head_dim) <= cap) {
+      SegPlan pl;
+      pl.seg = (int32_t)seg;
+      pl.partial_rows = p;
+      return pl;
+    }
+  }
+  return none;
+}
+
 // Arguments of a prefill call, and the launch's entry table (row blocks of
-// kPrefillRows rows per kv head, in entry order).
+// kPrefillRows rows per kv head, in entry order, each in nseg units).
 rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                         const int32_t *bt, int32_t bt_stride, int32_t n_seqs,
                         const rkv_prefill_args *a, const char *op, rkv::PrefillLaunch &pf) {
@@ -684,7 +763,15 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   std::stable_sort(order, order + a->n_seqs, [&](int32_t x, int32_t y) {
     return (int64_t)a->ctx_lens[x] + a->q_rows[x] > (int64_t)a->ctx_lens[y] + a->q_rows[y];
   });
-  int64_t blocks = 0;
+  if (a->workspace && reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "workspace is not 256-byte aligned");
+  const SegPlan sp = plan_segments(g, a->q_heads, pf.tq, a->n_seqs, a->ctx_lens, a->q_rows,
+                                   a->segment_tokens, a->workspace ? a->workspace_bytes : 0);
+  const size_t ws_need = prefill_ws_bytes(sp.partial_rows, g->head_dim);
+  if (ws_need > 0 && (!a->workspace || a->workspace_bytes < ws_need))
+    return fail(RKV_ERR_INVALID_ARG, op, "segment_tokens=%d needs a %zu-byte workspace (have %zu)",
+                a->segment_tokens, ws_need, a->workspace ? a->workspace_bytes : (size_t)0);
+  int64_t blocks = 0, prow = 0;
   for (int32_t k = 0; k < a->n_seqs; ++k) {
     const int32_t e = order[k];
     const int32_t seq = a->seq_ids[e], c = a->ctx_lens[e], n = a->q_rows[e], off = a->q_offsets[e];
@@ -702,12 +789,23 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
     pf.ctx[k] = c;
     pf.rows[k] = n;
     pf.qoff[k] = off;
-    pf.first[k] = (int32_t)blocks;
-    blocks += (n + pf.tq - 1) / pf.tq;
+    pf.nseg[k] = segments_of(end, sp.seg);
+    pf.seg[k] = pf.nseg[k] > 1 ? sp.seg : 0;
+    pf.wsoff[k] = pf.nseg[k] > 1 ? prow : 0;
+    if (pf.nseg[k] > 1) prow += (int64_t)n * a->q_heads * pf.nseg[k];
+    pf.first[k] = (int32_t)std::min<int64_t>(blocks, INT32_MAX);
+    blocks += (int64_t)(n + pf.tq - 1) / pf.tq * pf.nseg[k];
+  }
+  if (ws_need > 0) {
+    pf.ws_ml = static_cast<float *>(a->workspace);
+    pf.ws_o = reinterpret_cast<float *>(static_cast<uint8_t *>(a->workspace) +
+                                        ws_need - (size_t)prow * g->head_dim * 4);
   }
   pf.first[a->n_seqs] = (int32_t)blocks;
   if (blocks > 0 && (!a->q || !a->out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL q/out");
   if (blocks > (int64_t)1 << 30) return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
+  if (blocks > 0 && (int64_t)a->total_rows * a->q_heads > INT32_MAX)
+    return fail(RKV_ERR_INVALID_ARG, op, "total_rows * q_heads exceeds 2^31");
   rkv::DecodeLaunch &d = pf.d;
   d.g = to_geo(g);
   d.pages = static_cast<const uint8_t *>(pages);
@@ -739,6 +837,19 @@ rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pa
     return s;
   hipError_t e = rkv::launch_prefill(pf, as_stream(stream));
   return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
+size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_args *a) {
+  if (!g || !a || check_geometry(g, "rkv_prefill_workspace_bytes") != RKV_OK) return 0;
+  if (a->n_seqs < 1 || a->n_seqs > RKV_PREFILL_MAX_SEQS || !a->ctx_lens || !a->q_rows) return 0;
+  if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0) return 0;
+  const int32_t G = a->q_heads / g->kv_heads;
+  if (rkv::kPrefillRows % G != 0) return 0;
+  for (int32_t e = 0; e < a->n_seqs; ++e)
+    if (a->ctx_lens[e] < 0 || a->q_rows[e] < 0) return 0;
+  const SegPlan sp = plan_segments(g, a->q_heads, rkv::kPrefillRows / G, a->n_seqs, a->ctx_lens,
+                                   a->q_rows, a->segment_tokens, SIZE_MAX);
+  return prefill_ws_bytes(sp.partial_rows, g->head_dim);
 }
 
 rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,

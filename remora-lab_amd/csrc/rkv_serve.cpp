@@ -23,6 +23,7 @@
 
 #include "../../include/rkv.h"
 #include "rkv_host.h"
+#include "rkv_launch.h"
 
 using rkv::host::fail;
 using rkv::host::hip_fail;
@@ -50,6 +51,8 @@ struct rkv_serve {
   uint32_t n_steps = 0;
   void *ws = nullptr;  // decode workspace for max_decode rows of the longest sequence
   size_t ws_bytes = 0;
+  void *pf_ws = nullptr;  // prefill split-K partials (the automatic split fits itself in it)
+  size_t pf_ws_bytes = 0;
 };
 
 namespace {
@@ -105,9 +108,18 @@ rkv_status rkv_serve_create(rkv_ctx *ctx, const rkv_serve_desc *desc, rkv_serve 
   a.q_heads = desc->q_heads;
   a.max_seq_len = desc->max_pages_per_seq * desc->page_tokens;
   s->ws_bytes = rkv_decode_workspace_bytes(&s->g, &a);
+  // prefill partials: about two units of 128 rows per workgroup slot, which
+  // the automatic split (about one unit per slot) fits in; layout (m, l)
+  // rows padded to 256 bytes, then o rows
+  const int64_t pf_rows = std::min<int64_t>(
+      (int64_t)desc->max_prefill_rows * desc->q_heads * rkv::kPrefillMaxSegs,
+      2LL * rkv::kComputeUnits * rkv::kPrefillWgsPerCu * rkv::kPrefillRows);
+  s->pf_ws_bytes =
+      pf_rows > 0 ? ((size_t)pf_rows * 8 + 255) / 256 * 256 + (size_t)pf_rows * desc->head_dim * 4 : 0;
   const size_t mbytes = sizeof(int32_t) * std::max<size_t>(meta_ints(*desc), 1);
   hipError_t e = hipSuccess;
   if ((s->ws_bytes > 0 && (e = hipMalloc(&s->ws, s->ws_bytes)) != hipSuccess) ||
+      (s->pf_ws_bytes > 0 && (e = hipMalloc(&s->pf_ws, s->pf_ws_bytes)) != hipSuccess) ||
       (e = hipMalloc(&s->d_meta, mbytes)) != hipSuccess ||
       (e = hipHostMalloc(&s->h_meta[0], mbytes, hipHostMallocDefault)) != hipSuccess ||
       (e = hipHostMalloc(&s->h_meta[1], mbytes, hipHostMallocDefault)) != hipSuccess ||
@@ -127,6 +139,7 @@ rkv_status rkv_serve_destroy(rkv_serve *s) {
   for (int i = 0; i < 2; ++i)
     if (s->meta_done[i]) (void)hipEventSynchronize(s->meta_done[i]);
   (void)hipFree(s->ws);
+  (void)hipFree(s->pf_ws);
   (void)hipFree(s->d_meta);
   for (int i = 0; i < 2; ++i) {
     if (s->h_meta[i]) (void)hipHostFree(s->h_meta[i]);
@@ -324,6 +337,8 @@ rkv_status rkv_serve_prefill(rkv_serve *s, int32_t layer, const void *q, const v
     pa.scale = scale;
     pa.out = out;
     pa.out_dtype = out_dtype;
+    pa.workspace = s->pf_ws;
+    pa.workspace_bytes = s->pf_ws_bytes;
     if (rkv_status st = rkv_pool_prefill(s->pool, layer, &pa, stream)) return st;
   }
   return RKV_OK;

@@ -27,8 +27,11 @@ def _oracle(rko, sc, seq, ctx, n, q, scale):
                             q[None], scale, 1024)[0]
 
 
-def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, seed=0):
-    """entries: (seq, ctx, n) with ctx + n <= the sequence's length."""
+def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, seed=0,
+         segment_tokens=None):
+    """entries: (seq, ctx, n) with ctx + n <= the sequence's length.
+    segment_tokens: None runs without a workspace (no split); otherwise the
+    call gets the workspace rkv_prefill_workspace_bytes asks for."""
     torch = _torch()
     rng = np.random.default_rng(seed)
     D = sc.D
@@ -42,7 +45,14 @@ def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, 
         qd = qd.to(torch.bfloat16)
     out = torch.full((total, Hq, D), float("nan"), device="cuda",
                      dtype=torch.bfloat16 if out_bf16 else torch.float32)
-    a = rkv.prefill_args([s for s, _, _ in entries], [c for _, c, _ in entries], rows, qd, out, scale)
+    ent = ([s for s, _, _ in entries], [c for _, c, _ in entries], rows, qd, out, scale)
+    a = rkv.prefill_args(*ent)
+    if segment_tokens is not None:
+        a = rkv.prefill_args(*ent, segment_tokens=segment_tokens)
+        nb = rkv.prefill_workspace_bytes(sc.g, a)
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+        a = rkv.prefill_args(*ent, segment_tokens=segment_tokens, workspace=ws)
+        _run.last_ws_bytes = nb
     rkv.prefill_q8(ctx_h, sc.g, sc.pages_d, sc.bt_d, len(sc.lens), a)
     ctx_h.sync()
     got = out.float().cpu().numpy()
@@ -78,6 +88,57 @@ def test_prefill_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16, out_bf16
                src_bf16=q_bf16)
     ent = [(i, c, n) for i, (c, n) in enumerate(entries)]
     _run(rkv, rko, ctx, sc, ent, Hq, 1.0 / np.sqrt(D), q_bf16, out_bf16, seed=D + PT)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,PT,entries,seg,out_bf16", [
+    # forced segments: 128 tokens (two pages), so every long row block has
+    # segments its early rows cannot see (fully masked partials)
+    (16, 2, 256, 64, [(1000, 70), (0, 40), (300, 17), (129, 128)], 128, False),
+    # half-tile pages, 32-token segments: the 64-segment cap raises the length
+    (8, 2, 128, 16, [(0, 300), (2500, 33), (31, 2)], 32, True),
+    # 256-token pages (segment rounded up to a page), G = 1 and G = 16
+    (16, 16, 128, 256, [(700, 150), (0, 7)], 100, False),
+    (32, 2, 128, 64, [(1500, 23), (0, 9)], 512, True),
+])
+def test_prefill_split_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, seg, out_bf16):
+    """Row blocks' causal ranges split into segments whose partials the
+    combine merges: the same rows as the unsplit launch, at the same bars."""
+    lens = [c + n + 1 for c, n in entries]
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=len(entries) + PT)
+    ent = [(i, c, n) for i, (c, n) in enumerate(entries)]
+    _run(rkv, rko, ctx, sc, ent, Hq, 1.0 / np.sqrt(D), out_bf16=out_bf16, seed=PT,
+         segment_tokens=seg)
+    assert _run.last_ws_bytes > 0
+
+
+def test_prefill_automatic_split(rkv, rko, ctx):
+    """One long-context chunk has too few row blocks to fill the chip: with
+    a workspace the launch splits by itself (workspace_bytes > 0) and the
+    rows match the oracle; without one it runs unsplit, to the same rows;
+    segment_tokens < 0 never splits; an explicit split that does not fit its
+    workspace is refused."""
+    torch = _torch()
+    Hq, Hkv, D, PT = 16, 2, 128, 64
+    c, n = 6000, 64
+    sc = Scene(rkv, rko, Hkv, D, PT, [c + n], seed=11)
+    got = _run(rkv, rko, ctx, sc, [(0, c, n)], Hq, 0.088, seed=12, segment_tokens=0)
+    assert _run.last_ws_bytes > 0
+    unsplit = _run(rkv, rko, ctx, sc, [(0, c, n)], Hq, 0.088, seed=12)
+    assert float(np.abs(got - unsplit).max()) <= 1e-5
+    q = torch.zeros((n, Hq, D), device="cuda")
+    out = torch.zeros_like(q)
+    assert rkv.prefill_workspace_bytes(
+        sc.g, rkv.prefill_args([0], [c], [n], q, out, 1.0, segment_tokens=-1)) == 0
+    a = rkv.prefill_args([0], [c], [n], q, out, 1.0, segment_tokens=256)
+    need = rkv.prefill_workspace_bytes(sc.g, a)
+    assert need > 0
+    small = torch.empty(need - 256, dtype=torch.uint8, device="cuda")
+    with pytest.raises(rkv.RkvError) as e:
+        rkv.prefill_q8(ctx, sc.g, sc.pages_d, sc.bt_d, 1,
+                       rkv.prefill_args([0], [c], [n], q, out, 1.0, segment_tokens=256,
+                                        workspace=small))
+    assert e.value.status == rkv.ERR_INVALID_ARG
+    ctx.sync()
 
 
 def test_prefill_entries_share_a_sequence(rkv, rko, ctx):
