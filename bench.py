@@ -63,7 +63,8 @@ def parse():
                     help="1 = the headline line (default); 2-5 = BASELINE.json's secondary configs; "
                          "6 = prefix-shared decode (forks + copy-on-write pages); "
                          "7 = chunked prefill attention; 8 = R4KV page spill/restore; "
-                         "9 = serving step through the adapter")
+                         "9 = serving step through the adapter; 10 = host-KV tier (pages in "
+                         "pinned host memory)")
     ap.add_argument("--layers", type=int, default=48, help="layer pools of config 4")
     ap.add_argument("--serve-layers", type=int, default=4, help="layers of config 9")
     ap.add_argument("--prefill-batch", type=int, default=8, help="sequences of config 7")
@@ -1057,6 +1058,132 @@ def run_config9(args) -> int:
     return 0
 
 
+def run_config10(args) -> int:
+    """Host-KV tier (research/host-kv/README.md:1-24): B=8 sequences of
+    L=32768 tokens whose pages live in pinned host memory (RKV_PAGES_HOST),
+    Hq=16, Hkv=2, D=256, page 64: 285 MB of Q8 K/V in one layer, read over
+    the host link by the same kernels as an HBM pool.  Modes, one launch a
+    step: decode (q_len 1: 8 query rows per kv head served by each staged
+    tile), causal verify q_len 2 and 4 (16 and 32 rows), and a 512-row
+    chunked prefill of one sequence (128 rows per tile; its 32 row blocks
+    fetch overlapping causal ranges).  `physical` = unique K/V bytes / time;
+    `logical` = bytes served to query rows / time (each fetched byte serves
+    the tile's rows).  Beside them: the link's read roof (rkv_stream_read
+    over the pinned pages, vector loads), a DMA copy of pinned memory to HBM,
+    and the same decode on an HBM pool.  `value` is the decode's logical
+    GB/s."""
+    import torch
+    rkv = load_rkv()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ctx = rkv.Ctx(0)
+    Hq, Hkv, D, PT = 16, 2, 256, 64
+    B, L = 8, 32768
+    G = Hq // Hkv
+    pps = L // PT
+    num_pages = int(math.ceil(B * pps * 1.10))
+    row = D // 32 * 34
+    kv_bytes = B * L * Hkv * 2 * row
+    stream = torch.cuda.current_stream()
+    pools = {}
+    for name, mem in (("host", rkv.PAGES_HOST), ("hbm", rkv.PAGES_DEVICE)):
+        pool = rkv.Pool(ctx, 1, Hkv, D, PT, num_pages, B, pps, seed=args.seed, page_memory=mem)
+        for s_ in range(B):
+            pool.alloc.reserve(s_, L)
+        pool.sync_tables()
+        _fill_layer(rkv, pool, 0, range(B), [L] * B, Hkv, D, args.seed)
+        pools[name] = pool
+    ctx.sync()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed + 10)
+    sid = torch.arange(B, device=dev, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(D)
+
+    def timed(launch, reps):
+        for _ in range(2):
+            launch()
+        torch.cuda.synchronize()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * reps)]
+        for r in range(reps):
+            ev[2 * r].record(stream)
+            launch()
+            ev[2 * r + 1].record(stream)
+        torch.cuda.synchronize()
+        ts = sorted(ev[2 * r].elapsed_time(ev[2 * r + 1]) * 1e-3 for r in range(reps))
+        return ts[reps // 2]
+
+    modes = {}
+    reps = max(args.steps // 4, 3)
+    for pname in ("host", "hbm"):
+        pool = pools[pname]
+        for q_len in ((1, 2, 4) if pname == "host" else (1,)):
+            q = torch.randn((B, q_len, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+            out = torch.empty((B, q_len, Hq, D), device=dev, dtype=torch.float32)
+            a = rkv.decode_args(q, out, sid, scale, L, q_len=q_len)
+            ws = torch.empty(max(rkv.decode_workspace_bytes(pool.geometry, a), 4), dtype=torch.uint8,
+                             device=dev)
+            a = rkv.decode_args(q, out, sid, scale, L, q_len=q_len, workspace=ws)
+            t = timed(lambda: pool.decode(0, a, stream=stream), reps)
+            rows = G * q_len
+            modes[f"{pname}_q_len{q_len}"] = {
+                "us": round(t * 1e6, 1), "rows_per_tile": rows,
+                "physical_gbs": round(kv_bytes / t / 1e9, 2),
+                "logical_gbs": round(kv_bytes * rows / t / 1e9, 2)}
+    # chunked prefill of sequence 0's last 512 tokens over the host pages
+    N = 512
+    qp = torch.randn((N, Hq, D), generator=gen, device=dev).to(torch.bfloat16)
+    op = torch.empty((N, Hq, D), device=dev, dtype=torch.float32)
+    ent = ([0], [L - N], [N], qp, op, scale)
+    pws_bytes = rkv.prefill_workspace_bytes(pools["host"].geometry, rkv.prefill_args(*ent))
+    pws = torch.empty(max(pws_bytes, 1), dtype=torch.uint8, device=dev)
+    pa = rkv.prefill_args(*ent, workspace=pws)
+    t = timed(lambda: pools["host"].prefill(0, pa, stream=stream), reps)
+    tq = 128 // G
+    seq_bytes = L * Hkv * 2 * row
+    fetched = sum((L - N + min(tq * (b + 1), N)) * Hkv * 2 * row for b in range(N // tq))
+    modes["host_prefill512"] = {
+        "us": round(t * 1e6, 1), "rows_per_tile": 128, "split_workspace_bytes": pws_bytes,
+        "physical_gbs": round(seq_bytes / t / 1e9, 2),
+        "block_fetch_gbs": round(fetched / t / 1e9, 2),
+        "logical_gbs": round(fetched * 128 / t / 1e9, 2)}
+    # the link's read roof and a DMA copy, beside the kernels
+    word = torch.zeros(1, dtype=torch.int32, device=dev)
+    base = pools["host"].layer_pages(0)
+    nread = kv_bytes // 16 * 16
+    roof = {}
+    for blocks in (256, 1024):
+        tr = timed(lambda: rkv.stream_read(ctx, int(base), 0, blocks, word, nbytes=nread,
+                                           stream=stream), 3)
+        roof[blocks] = nread / tr / 1e9
+    src = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    tc = timed(lambda: dst.copy_(src, non_blocking=True), 5)
+    dec = modes["host_q_len1"]
+    res = {
+        "metric": "config 10: host-KV tier decode, logical GB/s (K/V bytes x rows served per "
+                  "fetched byte) over pages in pinned host memory",
+        "value": dec["logical_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": reps,
+        "warmup": 2, "ms_per_step": round(dec["us"] / 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 QK (two q planes) + f16 PV (two-term weights), f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
+        "config": {"workload": (f"host-KV tier: B={B}, L={L}, Hq={Hq}, Hkv={Hkv}, D={D}, page {PT}, "
+                                f"pages in pinned host memory ({kv_bytes} K/V bytes); decode, verify "
+                                f"q_len 2/4, 512-row prefill"),
+                   "batch": B, "seq_len": L},
+        "modes": modes,
+        "link_read_roof_gbs": round(max(roof.values()), 2),
+        "link_read_roof_blocks": max(roof, key=roof.get),
+        "dma_h2d_copy_gbs": round((256 << 20) / tc / 1e9, 2),
+        "hbm_pool_decode_us": modes["hbm_q_len1"]["us"],
+    }
+    print(json.dumps(res), flush=True)
+    for pool in pools.values():
+        pool.close()
+    ctx.close()
+    return 0
+
+
 def run_config8(args) -> int:
     """Off-HBM tier (R4KV pages): a 4096-token range of one sequence over 48
     layers (Hkv=2, D=256, page 64) is one page of 214 MB.  Timed, with HIP
@@ -1139,6 +1266,8 @@ def run_config8(args) -> int:
 
 if __name__ == "__main__":
     _a = parse()
+    if _a.config == 10:
+        sys.exit(run_config10(_a))
     if _a.config == 8:
         sys.exit(run_config8(_a))
     if _a.config == 7:

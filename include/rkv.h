@@ -340,6 +340,15 @@ rkv_status rkv_flash_decode_q8(rkv_ctx *ctx, const rkv_flash_decode_params *p,
  * The operator-level API a serving adapter (BatchStepModel, adapter.rs:28-72)
  * would hold per model.  Block-table edits made through the allocator are
  * uploaded by rkv_pool_sync_tables() before the next launch. */
+/* Where a pool's pages live.  RKV_PAGES_HOST puts them in pinned host
+ * memory mapped for the device (the reference's host-KV tier,
+ * research/host-kv/README.md:1-24): every kernel reads and writes them
+ * over the host link instead of HBM, and each K/V tile a kernel stages in
+ * LDS still serves every query row of its kv head (the GQA group times
+ * q_len, or a prefill block's 128 rows), so the rows served per fetched
+ * byte multiply the link's bandwidth. */
+#define RKV_PAGES_DEVICE 0
+#define RKV_PAGES_HOST 1
 typedef struct rkv_pool_desc {
   int32_t layers;
   int32_t kv_heads;
@@ -349,6 +358,7 @@ typedef struct rkv_pool_desc {
   int32_t max_seqs;
   int32_t max_pages_per_seq;
   uint64_t free_list_seed;
+  int32_t page_memory;  /* RKV_PAGES_DEVICE (0) | RKV_PAGES_HOST */
 } rkv_pool_desc;
 typedef struct rkv_pool rkv_pool;
 rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **out);
@@ -362,7 +372,8 @@ rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
  * before last is still in flight.  Use one stream for a pool's syncs and
  * launches. */
 rkv_status rkv_pool_sync_tables(rkv_pool *pool, void *stream);
-/* Device pointers owned by the pool. */
+/* Device pointers owned by the pool (for a host-memory pool, the device
+ * mapping of its pinned pages). */
 void *rkv_pool_layer_pages(rkv_pool *pool, int32_t layer);
 const int32_t *rkv_pool_block_tables(rkv_pool *pool); /* [max_seqs][max_pages_per_seq] */
 const int32_t *rkv_pool_seq_lens(rkv_pool *pool);     /* [max_seqs] */
@@ -509,6 +520,7 @@ typedef struct rkv_serve_desc {
   int32_t max_prefill_rows;   /* prefill query rows per step, >= 0 */
   int32_t rule;               /* RKV_Q8_CANONICAL | RKV_Q8_HARSERVE */
   uint64_t free_list_seed;
+  int32_t page_memory;        /* RKV_PAGES_DEVICE (0) | RKV_PAGES_HOST */
 } rkv_serve_desc;
 
 /* One sequence in one step. */

@@ -108,7 +108,7 @@ class ServeDesc(C.Structure):
                 ("page_tokens", C.c_int32), ("num_pages", C.c_int32), ("max_seqs", C.c_int32),
                 ("max_pages_per_seq", C.c_int32), ("q_heads", C.c_int32),
                 ("max_decode", C.c_int32), ("max_prefill_rows", C.c_int32), ("rule", C.c_int32),
-                ("free_list_seed", C.c_uint64)]
+                ("free_list_seed", C.c_uint64), ("page_memory", C.c_int32)]
 
 
 class ServeEntry(C.Structure):
@@ -124,7 +124,11 @@ class PageLocation(C.Structure):
 class PoolDesc(C.Structure):
     _fields_ = [("layers", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
                 ("page_tokens", C.c_int32), ("num_pages", C.c_int32), ("max_seqs", C.c_int32),
-                ("max_pages_per_seq", C.c_int32), ("free_list_seed", C.c_uint64)]
+                ("max_pages_per_seq", C.c_int32), ("free_list_seed", C.c_uint64),
+                ("page_memory", C.c_int32)]
+
+
+PAGES_DEVICE, PAGES_HOST = 0, 1
 
 
 _SIGS = {
@@ -593,10 +597,10 @@ class Pool:
     """Device pages for `layers` layers + allocator + device block tables."""
 
     def __init__(self, ctx: Ctx, layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
-                 max_pages_per_seq, seed=0):
+                 max_pages_per_seq, seed=0, page_memory=0):
         self.ctx = ctx
         d = PoolDesc(layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
-                     max_pages_per_seq, seed)
+                     max_pages_per_seq, seed, page_memory)
         h = P()
         check(lib().rkv_pool_create(ctx.h, C.byref(d), C.byref(h)))
         self.h = h
@@ -687,10 +691,11 @@ class Serve:
 
     def __init__(self, ctx: Ctx, layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
                  max_pages_per_seq, q_heads, max_decode, max_prefill_rows, rule=Q8_CANONICAL,
-                 seed=0):
+                 seed=0, page_memory=0):
         self.ctx = ctx
         d = ServeDesc(layers, kv_heads, head_dim, page_tokens, num_pages, max_seqs,
-                      max_pages_per_seq, q_heads, max_decode, max_prefill_rows, rule, seed)
+                      max_pages_per_seq, q_heads, max_decode, max_prefill_rows, rule, seed,
+                      page_memory)
         h = P()
         check(lib().rkv_serve_create(ctx.h, C.byref(d), C.byref(h)))
         self.h = h

@@ -518,17 +518,19 @@ struct Plan {
   int32_t n_wg = 0;     // grid.x: upper bound of the batch's partition count
   int32_t n_parts = 0;  // explicit: ceil(max_len / pt)
   bool direct = false;  // one partition covers every sequence: no partials
+  int32_t stages = 2;   // LDS ring depth of the launch
 };
 
-Plan plan_of(const rkv_kv_geometry *g, const rkv_decode_args *a) {
+Plan plan_of(const rkv_kv_geometry *g, const rkv_decode_args *a, int32_t stages) {
   Plan pl;
+  pl.stages = stages;
   pl.unit = std::max<int32_t>(32, g->page_tokens);
   pl.kmin = (256 + pl.unit - 1) / pl.unit;
   pl.kmax = 64 * g->page_tokens / pl.unit;
   pl.max_len = std::max<int32_t>(a->max_seq_len, 1);
   const int32_t rows = a->q_len * (a->q_heads / std::max(g->kv_heads, 1));
   const int64_t slots = (int64_t)rkv::kComputeUnits *
-                        rkv::decode_wgs_per_cu(g->head_dim, rows, decode_stages());
+                        rkv::decode_wgs_per_cu(g->head_dim, rows, stages);
   pl.target = (int32_t)std::max<int64_t>(1, slots / g->kv_heads);
   const int64_t B = std::max<int32_t>(a->batch, 0);
   if (a->partition_tokens > 0) {
@@ -624,7 +626,7 @@ rkv::DecodeLaunch make_decode(rkv_ctx *ctx, const rkv_kv_geometry *g, const void
   d.out = a->out;
   d.out_bf16 = a->out_dtype == RKV_BF16;
   d.fault = ctx->d_fault;
-  d.stages = decode_stages();
+  d.stages = pl.stages;
   if (const rkv_append_args *ap = a->append; ap && ap->n_rows > 0) {
     d.pages_w = static_cast<uint8_t *>(const_cast<void *>(pages));
     d.app_seq_ids = ap->seq_ids;
@@ -894,20 +896,25 @@ int32_t rkv_decode_partition_tokens(const rkv_kv_geometry *g, const rkv_decode_a
 size_t rkv_decode_workspace_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a) {
   if (!g || !a || check_geometry(g, "rkv_decode_workspace_bytes") != RKV_OK) return 0;
   if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0 || a->q_len < 1) return 0;
-  return ws_bytes(g, a, plan_of(g, a));
+  // enough for either ring depth (a pool in host memory launches 3 stages)
+  return std::max(ws_bytes(g, a, plan_of(g, a, 2)), ws_bytes(g, a, plan_of(g, a, 3)));
 }
 
-rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
-                         const int32_t *block_tables, int32_t bt_stride,
-                         const int32_t *seq_lens, int32_t n_seqs, const rkv_decode_args *a,
-                         void *stream) {
+}  // extern "C"
+
+namespace {
+// rkv_decode_q8 with an explicit LDS ring depth: 2 (the default, K codes in
+// registers) or 3 (K codes staged in LDS with V, two tiles in flight).
+rkv_status decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                     const int32_t *block_tables, int32_t bt_stride, const int32_t *seq_lens,
+                     int32_t n_seqs, const rkv_decode_args *a, void *stream, int32_t stages) {
   const char *op = "rkv_decode_q8";
   if (rkv_status s = use_device(ctx, op)) return s;
   if (rkv_status s = check_decode(g, a, op)) return s;
   if (rkv_status s = check_tables(pages, block_tables, bt_stride, n_seqs, op)) return s;
   if (!seq_lens) return fail(RKV_ERR_INVALID_ARG, op, "seq_lens is NULL");
   if (a->batch == 0) return RKV_OK;
-  const Plan pl = plan_of(g, a);
+  const Plan pl = plan_of(g, a, stages);
   rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pl);
   hipStream_t hs = as_stream(stream);
   if (!pl.direct) {
@@ -936,6 +943,17 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
   }
   return RKV_OK;
 }
+}  // namespace
+
+extern "C" {
+
+rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                         const int32_t *block_tables, int32_t bt_stride,
+                         const int32_t *seq_lens, int32_t n_seqs, const rkv_decode_args *a,
+                         void *stream) {
+  return decode_q8(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, stream,
+                   decode_stages());
+}
 
 rkv_status rkv_decode_q8_partials(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                                   const int32_t *block_tables, int32_t bt_stride,
@@ -950,7 +968,7 @@ rkv_status rkv_decode_q8_partials(rkv_ctx *ctx, const rkv_kv_geometry *g, const 
     return fail(RKV_ERR_INVALID_ARG, op, "needs an explicit partition_tokens (the [B][rows][n_parts] "
                                          "layout is sized by it)");
   if (a->batch == 0) return RKV_OK;
-  const Plan pl = plan_of(g, a);
+  const Plan pl = plan_of(g, a, decode_stages());
   rkv::DecodeLaunch d = make_decode(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, pl);
   d.ws_ml = ml;  // per-entry layout, written even for one partition
   d.ws_o = o;
@@ -1153,7 +1171,8 @@ struct rkv_pool {
   rkv_pool_desc d{};
   rkv_kv_geometry g{};
   rkv_alloc *alloc = nullptr;
-  uint8_t *pages = nullptr;  // layers * num_pages * page_bytes
+  uint8_t *pages = nullptr;  // layers * num_pages * page_bytes (device address)
+  void *host_pages = nullptr;  // RKV_PAGES_HOST: the pinned allocation behind `pages`
   size_t layer_bytes = 0;
   int32_t *d_tables = nullptr;
   int32_t *d_lens = nullptr;
@@ -1184,6 +1203,8 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
   if (!desc || !out) return fail(RKV_ERR_INVALID_ARG, op, "NULL argument");
   *out = nullptr;
   if (desc->layers < 1) return fail(RKV_ERR_INVALID_ARG, op, "layers=%d", desc->layers);
+  if (desc->page_memory != RKV_PAGES_DEVICE && desc->page_memory != RKV_PAGES_HOST)
+    return fail(RKV_ERR_INVALID_ARG, op, "page_memory=%d", desc->page_memory);
   rkv_kv_geometry g{desc->kv_heads, desc->head_dim, desc->page_tokens, desc->num_pages};
   if (rkv_status s = check_geometry(&g, op)) return s;
   rkv_alloc_desc ad{desc->num_pages, desc->page_tokens, desc->max_seqs, desc->max_pages_per_seq,
@@ -1200,7 +1221,23 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
   hipError_t e;
   const size_t tbytes = sizeof(int32_t) * (size_t)desc->max_seqs * desc->max_pages_per_seq;
   const size_t sbytes = sizeof(int32_t) * stage_ints(*desc);
-  if ((e = hipMalloc(&p->pages, p->layer_bytes * desc->layers)) != hipSuccess ||
+  const size_t all_pages = p->layer_bytes * desc->layers;
+  if (desc->page_memory == RKV_PAGES_HOST) {
+    // pinned, mapped for the device; non-coherent, so the device may cache
+    // what it reads (the pages change only through this library's kernels)
+    if ((e = hipHostMalloc(&p->host_pages, all_pages,
+                           hipHostMallocMapped | hipHostMallocNonCoherent)) != hipSuccess ||
+        (e = hipHostGetDevicePointer(reinterpret_cast<void **>(&p->pages), p->host_pages, 0)) !=
+            hipSuccess) {
+      rkv_status s = fail(RKV_ERR_DEVICE, op, "allocating %zu pinned host page bytes: %s",
+                          all_pages, hipGetErrorString(e));
+      rkv_pool_destroy(p);
+      return s;
+    }
+    std::memset(p->host_pages, 0, all_pages);
+  }
+  if ((desc->page_memory == RKV_PAGES_DEVICE &&
+       (e = hipMalloc(&p->pages, all_pages)) != hipSuccess) ||
       (e = hipMalloc(&p->d_tables, tbytes)) != hipSuccess ||
       (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess ||
       (e = hipMalloc(&p->d_stage, sbytes)) != hipSuccess ||
@@ -1216,7 +1253,7 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
     return s;
   }
   // zeroed pages: never-written slots hold finite codes and scales
-  if ((e = hipMemset(p->pages, 0, p->layer_bytes * desc->layers)) != hipSuccess) {
+  if (desc->page_memory == RKV_PAGES_DEVICE && (e = hipMemset(p->pages, 0, all_pages)) != hipSuccess) {
     rkv_pool_destroy(p);
     return hip_fail(op, e);
   }
@@ -1238,7 +1275,8 @@ rkv_status rkv_pool_destroy(rkv_pool *p) {
   for (int i = 0; i < 2; ++i) {
     if (p->stage_done[i]) (void)hipEventSynchronize(p->stage_done[i]);
   }
-  (void)hipFree(p->pages);
+  if (p->host_pages) (void)hipHostFree(p->host_pages);
+  else (void)hipFree(p->pages);
   (void)hipFree(p->d_tables);
   (void)hipFree(p->d_lens);
   (void)hipFree(p->d_stage);
@@ -1321,8 +1359,11 @@ rkv_status rkv_pool_decode(rkv_pool *p, int32_t layer, const rkv_decode_args *ar
   const char *op = "rkv_pool_decode";
   if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
   if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
-  return rkv_decode_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
-                       p->d.max_pages_per_seq, p->d_lens, p->d.max_seqs, args, stream);
+  // pages in host memory: K staged through LDS with V (the register loads
+  // of K read the host link at 87% of the LDS-DMA copies' rate)
+  return decode_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
+                   p->d.max_pages_per_seq, p->d_lens, p->d.max_seqs, args, stream,
+                   p->d.page_memory == RKV_PAGES_HOST ? 3 : decode_stages());
 }
 
 rkv_status rkv_pool_prefill(rkv_pool *p, int32_t layer, const rkv_prefill_args *args,

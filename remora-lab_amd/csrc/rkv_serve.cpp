@@ -89,7 +89,7 @@ rkv_status rkv_serve_create(rkv_ctx *ctx, const rkv_serve_desc *desc, rkv_serve 
     return fail(RKV_ERR_INVALID_ARG, op, "rule=%d", desc->rule);
   rkv_pool_desc pd{desc->layers,    desc->kv_heads, desc->head_dim,
                    desc->page_tokens, desc->num_pages, desc->max_seqs,
-                   desc->max_pages_per_seq, desc->free_list_seed};
+                   desc->max_pages_per_seq, desc->free_list_seed, desc->page_memory};
   rkv_serve *s = new rkv_serve;
   s->ctx = ctx;
   s->d = *desc;
