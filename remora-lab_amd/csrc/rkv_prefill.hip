@@ -34,15 +34,19 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
-  // entry and unit of this workgroup (the table is in the kernel
-  // arguments); an entry's units are taken last first (longest causal range
-  // first, as the entries themselves are ordered)
-  const int32_t x = (int32_t)blockIdx.x;
+  // kv head, entry and unit of this workgroup (the table is in the kernel
+  // arguments).  The kv heads of a unit are dispatched together, and an
+  // entry's units go segment by segment, each segment's row blocks last
+  // first: with the entries ordered by causal extent, units are taken about
+  // longest first (every segment but a block's last is seg tokens long).
+  const int kvh = (int)(blockIdx.x % (unsigned)g.kv_heads);
+  const int32_t x = (int32_t)(blockIdx.x / (unsigned)g.kv_heads);
   int e = 0;
   while (e + 1 < pf.n_entries && x >= pf.first[e + 1]) ++e;
-  const int32_t u = pf.first[e + 1] - 1 - x;
   const int32_t ns = pf.nseg[e];
-  const int32_t rb = u / ns, sg = u % ns;
+  const int32_t nb = (pf.first[e + 1] - pf.first[e]) / ns;  // row blocks of the entry
+  const int32_t v = x - pf.first[e];
+  const int32_t sg = v / nb, rb = nb - 1 - v % nb;
   const int32_t seq = pf.seq[e], ctx = pf.ctx[e], n = pf.rows[e];
   const int32_t j0 = pf.tq * rb;
   const int32_t jn = min(pf.tq, n - j0);
@@ -85,7 +89,6 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.li = dc.lane & 15;
   dc.lg = dc.lane >> 4;
   const int lane = dc.lane, li = dc.li, lg = dc.lg;
-  const int kvh = blockIdx.y;
   const int r0 = 16 * dc.wave;
   dc.kvh = kvh;
   dc.b = e;
@@ -208,7 +211,7 @@ __global__ __launch_bounds__(64) void prefill_combine_kernel(PrefillCombine c) {
 
 template <int D, int NS>
 hipError_t launch_prefill_t(const PrefillLaunch &pf, hipStream_t s) {
-  dim3 grid((unsigned)pf.first[pf.n_entries], (unsigned)pf.d.g.kv_heads);
+  dim3 grid((unsigned)pf.first[pf.n_entries] * (unsigned)pf.d.g.kv_heads);
   if (pf.d.g.page_tokens < kTile)
     hipLaunchKernelGGL((prefill_kernel<D, true, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
   else

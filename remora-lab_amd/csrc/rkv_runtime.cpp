@@ -10,6 +10,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -668,6 +669,102 @@ size_t prefill_ws_bytes(int64_t partial_rows, int32_t head_dim) {
   return ml + (size_t)partial_rows * head_dim * 4;
 }
 
+constexpr int64_t kUnitCost = 64;       // tokens: a unit's prologue and epilogue
+constexpr int64_t kSplitUnitCost = 32;  // tokens: a split unit's partial rows
+constexpr int64_t kMaxSimUnits = 16384; // units (times kv heads) a plan simulates at most
+
+// Makespan, in tokens of causal range, of the launch's units dispatched in
+// the kernel's order (entries by `order`, each entry segment by segment and
+// each segment's row blocks last first, the kv heads of a unit together),
+// each unit going to the compute unit that frees first.  One prefill
+// workgroup keeps a CU about as busy as two, so a CU's time is the sum of
+// its units'.
+int64_t simulate_prefill(const int32_t *ctx, const int32_t *rows, const int32_t *order, int32_t n,
+                         int32_t tq, int32_t kv_heads, int64_t seg) {
+  std::vector<int64_t> load(rkv::kComputeUnits, 0);  // min-heap
+  const auto later = std::greater<int64_t>();
+  for (int32_t k = 0; k < n; ++k) {
+    const int64_t c = ctx[order[k]], r = rows[order[k]];
+    const int64_t nb = (r + tq - 1) / tq;
+    const int32_t ns = segments_of(c + r, (int32_t)seg);
+    for (int32_t sg = 0; sg < ns; ++sg)
+      for (int64_t b = nb - 1; b >= 0; --b) {
+        const int64_t range = c + std::min<int64_t>(tq * (b + 1), r);
+        const int64_t len = ns == 1 ? range : std::clamp<int64_t>(range - sg * seg, 0, seg);
+        const int64_t cost = len + kUnitCost + (ns > 1 ? kSplitUnitCost : 0);
+        for (int32_t h = 0; h < kv_heads; ++h) {
+          std::pop_heap(load.begin(), load.end(), later);
+          load.back() += cost;
+          std::push_heap(load.begin(), load.end(), later);
+        }
+      }
+  }
+  return *std::max_element(load.begin(), load.end());
+}
+
+// The automatic split.  A launch whose units do not divide evenly over the
+// CUs -- too few row blocks, or a few long causal ranges among short ones --
+// ends when its longest units do; cutting every range longer than a segment
+// into segments evens the CUs' loads.  Candidates: the longest range in k
+// segments for a few k; the plan is memoized for the next call with the same
+// entries (a serving step repeats them for every layer).
+template <typename RowsFor>
+SegPlan auto_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int32_t n,
+                      const int32_t *ctx_lens, const int32_t *q_rows, size_t cap,
+                      int64_t max_range, int64_t seg_floor, RowsFor rows_for) {
+  SegPlan none;
+  thread_local std::vector<int64_t> memo_key;
+  thread_local SegPlan memo_plan;
+  std::vector<int64_t> key = {tq, q_heads, g->kv_heads, g->page_tokens, g->head_dim,
+                              (int64_t)std::min<size_t>(cap, INT64_MAX), n};
+  for (int32_t e = 0; e < n; ++e) {
+    key.push_back(ctx_lens[e]);
+    key.push_back(q_rows[e]);
+  }
+  if (key == memo_key) return memo_plan;
+  int32_t order[RKV_PREFILL_MAX_SEQS];
+  int64_t units = 0;
+  for (int32_t e = 0; e < n; ++e) {
+    order[e] = e;
+    if (ctx_lens[e] < 0 || q_rows[e] < 0) return none;  // refused by the caller
+    units += ((int64_t)q_rows[e] + tq - 1) / tq;
+  }
+  std::stable_sort(order, order + n, [&](int32_t x, int32_t y) {
+    return (int64_t)ctx_lens[x] + q_rows[x] > (int64_t)ctx_lens[y] + q_rows[y];
+  });
+  SegPlan best = none;
+  if (units > 0 && units * g->kv_heads <= kMaxSimUnits / 4) {
+    const int64_t unit = std::max<int32_t>(32, g->page_tokens);
+    auto round_up = [&](int64_t t) { return (t + unit - 1) / unit * unit; };
+    const int64_t base = simulate_prefill(ctx_lens, q_rows, order, n, tq, g->kv_heads, 0);
+    int64_t best_t = base;
+    int64_t last = -1;
+    for (int64_t k : {2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64}) {
+      const int64_t seg = std::max<int64_t>({round_up((max_range + k - 1) / k),
+                                             round_up(kPrefillMinSegment), seg_floor});
+      if (seg >= max_range || seg == last) continue;
+      last = seg;
+      int64_t su = 0;
+      for (int32_t e = 0; e < n; ++e)
+        su += ((int64_t)q_rows[e] + tq - 1) / tq *
+              segments_of((int64_t)ctx_lens[e] + q_rows[e], (int32_t)seg);
+      if (su * g->kv_heads > kMaxSimUnits) continue;
+      const int64_t p = rows_for(seg);
+      if (p == 0 || prefill_ws_bytes(p, g->head_dim) > cap) continue;
+      const int64_t t = simulate_prefill(ctx_lens, q_rows, order, n, tq, g->kv_heads, seg);
+      if (t < best_t) {
+        best_t = t;
+        best.seg = (int32_t)seg;
+        best.partial_rows = p;
+      }
+    }
+    if (best_t * 20 > base * 19) best = none;
+  }
+  memo_key = std::move(key);
+  memo_plan = best;
+  return best;
+}
+
 // cap: workspace bytes available to the automatic split.
 SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int32_t n,
                       const int32_t *ctx_lens, const int32_t *q_rows, int32_t request,
@@ -676,11 +773,9 @@ SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
   if (request < 0 || n <= 0) return none;
   const int64_t unit = std::max<int32_t>(32, g->page_tokens);
   auto round_up = [&](int64_t t) { return (t + unit - 1) / unit * unit; };
-  int64_t max_range = 0, blocks = 0;
-  for (int32_t e = 0; e < n; ++e) {
+  int64_t max_range = 0;
+  for (int32_t e = 0; e < n; ++e)
     max_range = std::max<int64_t>(max_range, (int64_t)ctx_lens[e] + q_rows[e]);
-    blocks += ((int64_t)q_rows[e] + tq - 1) / tq;
-  }
   auto rows_for = [&](int64_t seg) {
     int64_t p = 0;
     for (int32_t e = 0; e < n; ++e) {
@@ -697,33 +792,9 @@ SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
     if (pl.partial_rows == 0) pl.seg = 0;
     return pl;
   }
-  // automatic: only a launch with fewer row blocks than compute units.  One
-  // prefill workgroup keeps a CU about as busy as two, so a CU's time is the
-  // sum of its units: k equal segments a block take ceil(units*k/CUs)/k of
-  // the unsplit time.  The fewest segments reaching the least of that, when
-  // it saves a tenth at least.
-  const int64_t units = blocks * g->kv_heads;
-  const int64_t cus = rkv::kComputeUnits;
-  if (units <= 0 || units >= cus) return none;
-  const int64_t k_max = std::min<int64_t>(rkv::kPrefillMaxSegs, max_range / kPrefillMinSegment);
-  auto cost = [&](int64_t k) { return (double)((units * k + cus - 1) / cus) / (double)k; };
-  double least = 1.0;
-  for (int64_t k = 2; k <= k_max; ++k) least = std::min(least, cost(k));
-  if (least > 0.9) return none;
-  int64_t want = 2;
-  while (cost(want) > least * 1.0001) ++want;
-  int64_t seg = std::max<int64_t>({round_up((max_range + want - 1) / want),
-                                   round_up(kPrefillMinSegment), seg_floor});
-  for (; seg < max_range; seg *= 2) {
-    const int64_t p = rows_for(seg);
-    if (p > 0 && prefill_ws_bytes(p, g->head_dim) <= cap) {
-      SegPlan pl;
-      pl.seg = (int32_t)seg;
-      pl.partial_rows = p;
-      return pl;
-    }
-  }
-  return none;
+  // automatic: simulate the launch for a few segment lengths and keep the
+  // shortest makespan, if it beats the unsplit launch by a twentieth
+  return auto_segments(g, q_heads, tq, n, ctx_lens, q_rows, cap, max_range, seg_floor, rows_for);
 }
 
 // Arguments of a prefill call, and the launch's entry table (row blocks of
@@ -805,7 +876,7 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   }
   pf.first[a->n_seqs] = (int32_t)blocks;
   if (blocks > 0 && (!a->q || !a->out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL q/out");
-  if (blocks > (int64_t)1 << 30) return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
+  if (blocks * g->kv_heads > INT32_MAX) return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
   if (blocks > 0 && (int64_t)a->total_rows * a->q_heads > INT32_MAX)
     return fail(RKV_ERR_INVALID_ARG, op, "total_rows * q_heads exceeds 2^31");
   rkv::DecodeLaunch &d = pf.d;
