@@ -97,10 +97,10 @@ hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s);
 // at rows qoff[e].. of q/out ([rows][q_heads][head_dim]); row i attends
 // positions [0, ctx[e]+i].  A row block is tq query tokens x
 // q_heads/kv_heads heads = kPrefillRows rows; its causal range is split into
-// nseg[e] segments of seg[e] tokens.  Workgroup x of the grid
-// (first[n_entries], kv_heads) takes unit u = first[e+1] - 1 - x of the
-// entry with first[e] <= x < first[e+1]: row block u / nseg[e], segment
-// u % nseg[e].  An entry with one segment writes its rows normalized; a
+// nseg[e] segments of seg[e] tokens.  Entry e owns units [first[e]*H,
+// first[e+1]*H) of the launch (H = kv_heads), one per (segment, kv head,
+// row block).  Workgroups go to the 8 XCDs round robin; XCD x takes list
+// chunks x, x + 8, ... of xcd_chunk consecutive units.  An entry with one segment writes its rows normalized; a
 // split one writes per-segment partials (m, l) and o at partial row
 // wsoff[e] + (row * q_heads + head) * nseg[e] + segment, which
 // launch_prefill's combine merges into the rows.
@@ -110,6 +110,12 @@ constexpr int kPrefillMaxEntries = 64;
 constexpr int kPrefillMaxPages = 4096;  // page-list capacity of one unit (LDS)
 constexpr int kPrefillMaxSegs = 64;
 constexpr int kPrefillWgsPerCu = 2;  // the prefill kernel's launch bounds
+// xcd_chunk of a launch over HBM pages (a causal range's 32 row blocks per kv
+// head on 4 XCDs: 2% faster than 1 on config 7, 1% on the serving step; 16
+// unbalances the serving step's mixed lengths) and over host-memory pages
+// (one XCD per range: the link, not the CUs, is the bound)
+constexpr int kPrefillXcdChunkHbm = 8;
+constexpr int kPrefillXcdChunkHost = 32;
 struct PrefillLaunch {
   DecodeLaunch d;  // geometry, pages, tables, q, out, dtypes, scale, fault, stages
   int32_t tq;
@@ -122,6 +128,7 @@ struct PrefillLaunch {
   int32_t seg[kPrefillMaxEntries];     // tokens, a multiple of max(32, page_tokens)
   int64_t wsoff[kPrefillMaxEntries];   // first partial row of a split entry
   int32_t first[kPrefillMaxEntries + 1];
+  int32_t xcd_chunk;  // 1: plain round robin; more: row blocks of one range share an L2
   float *ws_ml;  // split partials: (m, l) [partial row][2] ...
   float *ws_o;   // ... and o [partial row][head_dim]
 };

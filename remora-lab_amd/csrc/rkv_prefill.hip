@@ -34,19 +34,27 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
-  // kv head, entry and unit of this workgroup (the table is in the kernel
-  // arguments).  The kv heads of a unit are dispatched together, and an
-  // entry's units go segment by segment, each segment's row blocks last
-  // first: with the entries ordered by causal extent, units are taken about
-  // longest first (every segment but a block's last is seg tokens long).
-  const int kvh = (int)(blockIdx.x % (unsigned)g.kv_heads);
-  const int32_t x = (int32_t)(blockIdx.x / (unsigned)g.kv_heads);
+  // Unit of this workgroup.  Units are listed entry by entry (the entries
+  // ordered by causal extent), an entry's segment by segment, a segment's kv
+  // head by kv head, and a (segment, kv head)'s row blocks last first, so
+  // they come about longest first (every segment but a block's last is seg
+  // tokens long).  Workgroups go to the 8 XCDs round robin, and each XCD
+  // takes chunks of xcd_chunk consecutive units (chunks xcd, xcd + 8, ...):
+  // with chunks of 32, the row blocks that read one causal range share that
+  // XCD's L2, which pays when the pages sit behind the host link.
+  const uint32_t C = (uint32_t)pf.xcd_chunk;
+  const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
+  const int64_t j = ((int64_t)xcd + 8 * (int64_t)(slot / C)) * C + slot % C;
+  const int32_t H = g.kv_heads;
+  if (j >= (int64_t)pf.first[pf.n_entries] * H) return;  // padding of the last chunks
   int e = 0;
-  while (e + 1 < pf.n_entries && x >= pf.first[e + 1]) ++e;
+  while (e + 1 < pf.n_entries && j >= (int64_t)pf.first[e + 1] * H) ++e;
   const int32_t ns = pf.nseg[e];
   const int32_t nb = (pf.first[e + 1] - pf.first[e]) / ns;  // row blocks of the entry
-  const int32_t v = x - pf.first[e];
-  const int32_t sg = v / nb, rb = nb - 1 - v % nb;
+  const int32_t v = (int32_t)(j - (int64_t)pf.first[e] * H);
+  const int32_t sg = v / (H * nb);
+  const int kvh = (v / nb) % H;
+  const int32_t rb = nb - 1 - v % nb;
   const int32_t seq = pf.seq[e], ctx = pf.ctx[e], n = pf.rows[e];
   const int32_t j0 = pf.tq * rb;
   const int32_t jn = min(pf.tq, n - j0);
@@ -211,7 +219,9 @@ __global__ __launch_bounds__(64) void prefill_combine_kernel(PrefillCombine c) {
 
 template <int D, int NS>
 hipError_t launch_prefill_t(const PrefillLaunch &pf, hipStream_t s) {
-  dim3 grid((unsigned)pf.first[pf.n_entries] * (unsigned)pf.d.g.kv_heads);
+  const int64_t units = (int64_t)pf.first[pf.n_entries] * pf.d.g.kv_heads;
+  const int64_t round = 8 * (int64_t)pf.xcd_chunk;
+  dim3 grid((unsigned)((units + round - 1) / round * round));
   if (pf.d.g.page_tokens < kTile)
     hipLaunchKernelGGL((prefill_kernel<D, true, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
   else

@@ -673,31 +673,33 @@ constexpr int64_t kUnitCost = 64;       // tokens: a unit's prologue and epilogu
 constexpr int64_t kSplitUnitCost = 32;  // tokens: a split unit's partial rows
 constexpr int64_t kMaxSimUnits = 16384; // units (times kv heads) a plan simulates at most
 
-// Makespan, in tokens of causal range, of the launch's units dispatched in
-// the kernel's order (entries by `order`, each entry segment by segment and
-// each segment's row blocks last first, the kv heads of a unit together),
-// each unit going to the compute unit that frees first.  One prefill
-// workgroup keeps a CU about as busy as two, so a CU's time is the sum of
-// its units'.
+// Makespan, in tokens of causal range, of the launch's units in the
+// kernel's list order (entries by `order`; an entry's units segment by
+// segment, kv head by kv head, row blocks last first).  Unit j runs on XCD
+// (j / xcd_chunk) % 8, on whichever of that XCD's CUs frees first.
+// One prefill workgroup keeps a CU about as busy as two, so a CU's time is
+// the sum of its units'.
 int64_t simulate_prefill(const int32_t *ctx, const int32_t *rows, const int32_t *order, int32_t n,
-                         int32_t tq, int32_t kv_heads, int64_t seg) {
-  std::vector<int64_t> load(rkv::kComputeUnits, 0);  // min-heap
+                         int32_t tq, int32_t kv_heads, int64_t seg, int32_t xcd_chunk) {
+  constexpr int kXcds = 8;
+  constexpr int kCusPerXcd = rkv::kComputeUnits / kXcds;
+  std::vector<int64_t> load(rkv::kComputeUnits, 0);  // kXcds min-heaps of kCusPerXcd
   const auto later = std::greater<int64_t>();
+  int64_t j = 0;
   for (int32_t k = 0; k < n; ++k) {
     const int64_t c = ctx[order[k]], r = rows[order[k]];
     const int64_t nb = (r + tq - 1) / tq;
     const int32_t ns = segments_of(c + r, (int32_t)seg);
     for (int32_t sg = 0; sg < ns; ++sg)
-      for (int64_t b = nb - 1; b >= 0; --b) {
-        const int64_t range = c + std::min<int64_t>(tq * (b + 1), r);
-        const int64_t len = ns == 1 ? range : std::clamp<int64_t>(range - sg * seg, 0, seg);
-        const int64_t cost = len + kUnitCost + (ns > 1 ? kSplitUnitCost : 0);
-        for (int32_t h = 0; h < kv_heads; ++h) {
-          std::pop_heap(load.begin(), load.end(), later);
-          load.back() += cost;
-          std::push_heap(load.begin(), load.end(), later);
+      for (int32_t h = 0; h < kv_heads; ++h)
+        for (int64_t b = nb - 1; b >= 0; --b, ++j) {
+          const int64_t range = c + std::min<int64_t>(tq * (b + 1), r);
+          const int64_t len = ns == 1 ? range : std::clamp<int64_t>(range - sg * seg, 0, seg);
+          auto first = load.begin() + (j / xcd_chunk) % kXcds * kCusPerXcd;
+          std::pop_heap(first, first + kCusPerXcd, later);
+          first[kCusPerXcd - 1] += len + kUnitCost + (ns > 1 ? kSplitUnitCost : 0);
+          std::push_heap(first, first + kCusPerXcd, later);
         }
-      }
   }
   return *std::max_element(load.begin(), load.end());
 }
@@ -711,12 +713,12 @@ int64_t simulate_prefill(const int32_t *ctx, const int32_t *rows, const int32_t 
 template <typename RowsFor>
 SegPlan auto_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int32_t n,
                       const int32_t *ctx_lens, const int32_t *q_rows, size_t cap,
-                      int64_t max_range, int64_t seg_floor, RowsFor rows_for) {
+                      int32_t xcd_chunk, int64_t max_range, int64_t seg_floor, RowsFor rows_for) {
   SegPlan none;
   thread_local std::vector<int64_t> memo_key;
   thread_local SegPlan memo_plan;
   std::vector<int64_t> key = {tq, q_heads, g->kv_heads, g->page_tokens, g->head_dim,
-                              (int64_t)std::min<size_t>(cap, INT64_MAX), n};
+                              (int64_t)std::min<size_t>(cap, INT64_MAX), xcd_chunk, n};
   for (int32_t e = 0; e < n; ++e) {
     key.push_back(ctx_lens[e]);
     key.push_back(q_rows[e]);
@@ -736,7 +738,7 @@ SegPlan auto_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
   if (units > 0 && units * g->kv_heads <= kMaxSimUnits / 4) {
     const int64_t unit = std::max<int32_t>(32, g->page_tokens);
     auto round_up = [&](int64_t t) { return (t + unit - 1) / unit * unit; };
-    const int64_t base = simulate_prefill(ctx_lens, q_rows, order, n, tq, g->kv_heads, 0);
+    const int64_t base = simulate_prefill(ctx_lens, q_rows, order, n, tq, g->kv_heads, 0, xcd_chunk);
     int64_t best_t = base;
     int64_t last = -1;
     for (int64_t k : {2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64}) {
@@ -751,7 +753,7 @@ SegPlan auto_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
       if (su * g->kv_heads > kMaxSimUnits) continue;
       const int64_t p = rows_for(seg);
       if (p == 0 || prefill_ws_bytes(p, g->head_dim) > cap) continue;
-      const int64_t t = simulate_prefill(ctx_lens, q_rows, order, n, tq, g->kv_heads, seg);
+      const int64_t t = simulate_prefill(ctx_lens, q_rows, order, n, tq, g->kv_heads, seg, xcd_chunk);
       if (t < best_t) {
         best_t = t;
         best.seg = (int32_t)seg;
@@ -768,7 +770,7 @@ SegPlan auto_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
 // cap: workspace bytes available to the automatic split.
 SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int32_t n,
                       const int32_t *ctx_lens, const int32_t *q_rows, int32_t request,
-                      size_t cap) {
+                      size_t cap, int32_t xcd_chunk) {
   SegPlan none;
   if (request < 0 || n <= 0) return none;
   const int64_t unit = std::max<int32_t>(32, g->page_tokens);
@@ -794,14 +796,17 @@ SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
   }
   // automatic: simulate the launch for a few segment lengths and keep the
   // shortest makespan, if it beats the unsplit launch by a twentieth
-  return auto_segments(g, q_heads, tq, n, ctx_lens, q_rows, cap, max_range, seg_floor, rows_for);
+  return auto_segments(g, q_heads, tq, n, ctx_lens, q_rows, cap, xcd_chunk, max_range, seg_floor,
+                       rows_for);
 }
 
 // Arguments of a prefill call, and the launch's entry table (row blocks of
-// kPrefillRows rows per kv head, in entry order, each in nseg units).
+// kPrefillRows rows per kv head, in entry order, each in nseg units);
+// xcd_chunk as in rkv::PrefillLaunch.
 rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                         const int32_t *bt, int32_t bt_stride, int32_t n_seqs,
-                        const rkv_prefill_args *a, const char *op, rkv::PrefillLaunch &pf) {
+                        const rkv_prefill_args *a, const char *op, int32_t xcd_chunk,
+                        rkv::PrefillLaunch &pf) {
   if (rkv_status s = check_geometry(g, op)) return s;
   if (rkv_status s = check_tables(pages, bt, bt_stride, n_seqs, op)) return s;
   if (!a) return fail(RKV_ERR_INVALID_ARG, op, "args is NULL");
@@ -839,7 +844,8 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   if (a->workspace && reinterpret_cast<uintptr_t>(a->workspace) % 256 != 0)
     return fail(RKV_ERR_INVALID_ARG, op, "workspace is not 256-byte aligned");
   const SegPlan sp = plan_segments(g, a->q_heads, pf.tq, a->n_seqs, a->ctx_lens, a->q_rows,
-                                   a->segment_tokens, a->workspace ? a->workspace_bytes : 0);
+                                   a->segment_tokens, a->workspace ? a->workspace_bytes : 0,
+                                   xcd_chunk);
   const size_t ws_need = prefill_ws_bytes(sp.partial_rows, g->head_dim);
   if (ws_need > 0 && (!a->workspace || a->workspace_bytes < ws_need))
     return fail(RKV_ERR_INVALID_ARG, op, "segment_tokens=%d needs a %zu-byte workspace (have %zu)",
@@ -875,6 +881,7 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
                                         ws_need - (size_t)prow * g->head_dim * 4);
   }
   pf.first[a->n_seqs] = (int32_t)blocks;
+  pf.xcd_chunk = xcd_chunk;
   if (blocks > 0 && (!a->q || !a->out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL q/out");
   if (blocks * g->kv_heads > INT32_MAX) return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
   if (blocks > 0 && (int64_t)a->total_rows * a->q_heads > INT32_MAX)
@@ -896,6 +903,19 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   return RKV_OK;
 }
 
+rkv_status prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                      const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
+                      const rkv_prefill_args *a, void *stream, int32_t xcd_chunk) {
+  const char *op = "rkv_prefill_q8";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  rkv::PrefillLaunch pf{};
+  if (rkv_status s =
+          make_prefill(ctx, g, pages, block_tables, bt_stride, n_seqs, a, op, xcd_chunk, pf))
+    return s;
+  hipError_t e = rkv::launch_prefill(pf, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
 }  // namespace
 
 extern "C" {
@@ -903,13 +923,8 @@ extern "C" {
 rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                           const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
                           const rkv_prefill_args *a, void *stream) {
-  const char *op = "rkv_prefill_q8";
-  if (rkv_status s = use_device(ctx, op)) return s;
-  rkv::PrefillLaunch pf{};
-  if (rkv_status s = make_prefill(ctx, g, pages, block_tables, bt_stride, n_seqs, a, op, pf))
-    return s;
-  hipError_t e = rkv::launch_prefill(pf, as_stream(stream));
-  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+  return prefill_q8(ctx, g, pages, block_tables, bt_stride, n_seqs, a, stream,
+                    rkv::kPrefillXcdChunkHbm);
 }
 
 size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_args *a) {
@@ -921,7 +936,7 @@ size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_a
   for (int32_t e = 0; e < a->n_seqs; ++e)
     if (a->ctx_lens[e] < 0 || a->q_rows[e] < 0) return 0;
   const SegPlan sp = plan_segments(g, a->q_heads, rkv::kPrefillRows / G, a->n_seqs, a->ctx_lens,
-                                   a->q_rows, a->segment_tokens, SIZE_MAX);
+                                   a->q_rows, a->segment_tokens, SIZE_MAX, rkv::kPrefillXcdChunkHbm);
   return prefill_ws_bytes(sp.partial_rows, g->head_dim);
 }
 
@@ -1451,8 +1466,12 @@ rkv_status rkv_pool_prefill(rkv_pool *p, int32_t layer, const rkv_prefill_args *
                     e, args->ctx_lens[e], args->q_rows[e], p->alloc->lens[seq], seq);
     }
   }
-  return rkv_prefill_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
-                        p->d.max_pages_per_seq, p->d.max_seqs, args, stream);
+  // pages behind the host link: the row blocks of one causal range share
+  // one XCD's L2 (in HBM, chunks of 8 spread them over 4 XCDs)
+  return prefill_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
+                    p->d.max_pages_per_seq, p->d.max_seqs, args, stream,
+                    p->d.page_memory == RKV_PAGES_HOST ? rkv::kPrefillXcdChunkHost
+                                                       : rkv::kPrefillXcdChunkHbm);
 }
 
 rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind, uint8_t *out,
