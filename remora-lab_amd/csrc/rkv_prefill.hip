@@ -42,7 +42,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   // takes chunks of xcd_chunk consecutive units (chunks xcd, xcd + 8, ...):
   // with chunks of 32, the row blocks that read one causal range share that
   // XCD's L2, which pays when the pages sit behind the host link.
-  const uint32_t C = (uint32_t)pf.xcd_chunk;
+  const uint32_t C = (uint32_t)max(pf.xcd_chunk, 1);
   const uint32_t xcd = blockIdx.x & 7u, slot = blockIdx.x >> 3;
   const int64_t j = ((int64_t)xcd + 8 * (int64_t)(slot / C)) * C + slot % C;
   const int32_t H = g.kv_heads;
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(64) void prefill_combine_kernel(PrefillCombine c) {
 template <int D, int NS>
 hipError_t launch_prefill_t(const PrefillLaunch &pf, hipStream_t s) {
   const int64_t units = (int64_t)pf.first[pf.n_entries] * pf.d.g.kv_heads;
-  const int64_t round = 8 * (int64_t)pf.xcd_chunk;
+  const int64_t round = 8 * (int64_t)std::max(pf.xcd_chunk, 1);
   dim3 grid((unsigned)((units + round - 1) / round * round));
   if (pf.d.g.page_tokens < kTile)
     hipLaunchKernelGGL((prefill_kernel<D, true, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);

@@ -179,3 +179,37 @@ def test_serve_refusals_change_nothing(rkv, ctx):
     sv.begin_step(prefill=[(3, 10)], decode=[(1, 1)])
     assert sv.seq_len(3) == 10 and sv.seq_len(1) == 101
     sv.close()
+
+
+def test_serve_long_context_chunk_splits(rkv, rko, ctx):
+    """A short chunk after a long cached prompt has too few row blocks to
+    fill the chip, so the adapter's prefill splits its causal ranges (the
+    plan asks for a workspace); its rows still match the oracle."""
+    torch = __import__("torch")
+    D, Hkv, Hq, PT = 128, 2, 16, 64
+    sv = rkv.Serve(ctx, 1, Hkv, D, PT, num_pages=80, max_seqs=2, max_pages_per_seq=70,
+                   q_heads=Hq, max_decode=2, max_prefill_rows=1024, seed=2)
+    m = _Model(rko, 1, Hkv, Hq, D)
+    m.admit(1)
+    rng = np.random.default_rng(31)
+    scale = 1.0 / math.sqrt(D)
+    for chunk in (1000, 1000, 1000, 64):
+        done = len(m.rows[1][0][0])
+        sv.begin_step(prefill=[(1, chunk)])
+        q = rng.standard_normal((chunk, Hq, D)).astype(np.float32)
+        k = rng.standard_normal((chunk, Hkv, D)).astype(np.float32)
+        v = rng.standard_normal((chunk, Hkv, D)).astype(np.float32)
+        out = torch.empty((chunk, Hq, D), dtype=torch.float32, device="cuda")
+        sv.prefill(0, torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(),
+                   torch.from_numpy(v).cuda(), out, scale)
+        ctx.sync()
+        m.append(1, 0, k, v)
+        got = out.cpu().numpy()
+        for j in (0, chunk // 2, chunk - 1):
+            want = m.attend(1, 0, done + j + 1, q[j], scale)
+            assert_close(got[j].reshape(-1), want, what=f"ctx {done} chunk {chunk} row {j}")
+    # the last call's plan: 4 row blocks x 2 kv heads over 256 CUs is split
+    qt = torch.empty((64, Hq, D))
+    a = rkv.prefill_args([0], [3000], [64], qt, qt, scale)
+    assert rkv.prefill_workspace_bytes(sv.geometry, a) > 0
+    sv.close()
