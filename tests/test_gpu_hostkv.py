@@ -154,3 +154,66 @@ def test_host_serve_steps_match_device(rkv, ctx):
                 assert_close(b, a, what=f"step {step} layer {i // 2}: host-page decode")
     for sv in svs:
         sv.close()
+
+
+def test_host_pool_r4kv_spill_and_restore(rkv, ctx):
+    """R4KV pages (r4kv/src/page.rs:101-252) from a host-memory pool: the
+    spilled page equals the HBM pool's byte for byte, and restoring it into
+    another sequence of the host pool reproduces the spilled rows (gathered
+    bytes equal)."""
+    torch = __import__("torch")
+    Hkv, D, PT, layers = 2, 256, 64, 2
+    lens = [260, 90]
+    W = 8
+    rng = np.random.default_rng(17)
+    data = [[(rng.standard_normal((L, Hkv, D)).astype(np.float32),
+              rng.standard_normal((L, Hkv, D)).astype(np.float32)) for L in lens]
+            for _ in range(layers)]
+    pools = []
+    for mem in (rkv.PAGES_DEVICE, rkv.PAGES_HOST):
+        pool = rkv.Pool(ctx, layers, Hkv, D, PT, 24, 4, W, seed=5, page_memory=mem)
+        for s, L in enumerate(lens):
+            pool.alloc.reserve(s, L)
+        pool.sync_tables()
+        for layer in range(layers):
+            for s, L in enumerate(lens):
+                k, v = (torch.from_numpy(x).cuda() for x in data[layer][s])
+                pool.append(layer, torch.full((L,), s, dtype=torch.int32, device="cuda"),
+                            torch.arange(L, dtype=torch.int32, device="cuda"), k, v)
+        pools.append(pool)
+    ctx.sync()
+    t0, count = 64, 130
+    hdr = rkv.R4kvHeader(prefix_digest=0x1234ABCD5678EF01, token_start=0, token_count=0,
+                         pos_start=t0, layer_lo=0, layer_hi=0, k_fmt=0, v_fmt=0, epoch=3,
+                         generation=9, payload_len=0, sketch_offset=0, flags=2)
+    pages = []
+    for pool in pools:
+        n = pool.r4kv_page_bytes(count, 0, layers - 1)
+        staging = torch.zeros(n + 64, dtype=torch.uint8, device="cuda")
+        page = torch.zeros(n, dtype=torch.uint8).pin_memory()
+        pool.spill(0, t0, count, 0, layers - 1, hdr, staging, page)
+        ctx.sync()
+        pages.append(page.numpy().tobytes())
+    assert pages[0] == pages[1], "host-pool R4KV page differs from the HBM pool's"
+    host = pools[1]
+    host.alloc.reserve(2, t0 + count)
+    host.sync_tables()
+    exp = rkv.R4kvExpect(prefix_digest=0x1234ABCD5678EF01, token_start=t0, pos_start=t0,
+                         layer_lo=0, layer_hi=layers - 1, k_fmt=1, v_fmt=1, check_generation=1,
+                         generation_min=9, generation_max=9)
+    staging = torch.zeros(len(pages[1]) + 64, dtype=torch.uint8, device="cuda")
+    host.restore(2, pages[1], exp, staging)
+    ctx.sync()
+    rb = rkv.row_bytes(D)
+    for layer in range(layers):
+        for kind in (0, 1):
+            a = torch.empty(Hkv * (t0 + count) * rb, dtype=torch.uint8, device="cuda")
+            b = torch.empty(Hkv * lens[0] * rb, dtype=torch.uint8, device="cuda")
+            host.gather(layer, 2, kind, a)
+            host.gather(layer, 0, kind, b)
+            ctx.sync()
+            got = a.cpu().numpy().reshape(Hkv, t0 + count, rb)[:, t0:]
+            want = b.cpu().numpy().reshape(Hkv, lens[0], rb)[:, t0:t0 + count]
+            assert np.array_equal(got, want), f"layer {layer} kind {kind}: restored rows"
+    for pool in pools:
+        pool.close()
