@@ -883,7 +883,9 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   pf.first[a->n_seqs] = (int32_t)blocks;
   pf.xcd_chunk = xcd_chunk;
   if (blocks > 0 && (!a->q || !a->out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL q/out");
-  if (blocks * g->kv_heads > INT32_MAX) return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
+  // the grid rounds units up to whole XCD chunk rounds (8 * xcd_chunk)
+  if (blocks * g->kv_heads > INT32_MAX - 8 * (int64_t)xcd_chunk)
+    return fail(RKV_ERR_INVALID_ARG, op, "too many row blocks");
   if (blocks > 0 && (int64_t)a->total_rows * a->q_heads > INT32_MAX)
     return fail(RKV_ERR_INVALID_ARG, op, "total_rows * q_heads exceeds 2^31");
   rkv::DecodeLaunch &d = pf.d;
