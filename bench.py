@@ -450,6 +450,12 @@ class _Decoder:
         import torch
         return int(self.ws[:4].view(torch.int32).item())
 
+    def partitions_total(self, batch) -> int:
+        """Partitions of the last launch over its `batch` entries (workspace
+        header: partition length, then first partition and count per entry)."""
+        import torch
+        return int(self.ws[:4 * (1 + 2 * batch)].view(torch.int32)[2::2].sum().item())
+
 
 def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extra):
     value = step_bytes / step_s / 1e9
@@ -607,7 +613,7 @@ def run_config(args) -> int:
         if args.graph:
             wall, launch = graph_wall, "hip graph per layer pool, replayed"
     pt = dec.partition_tokens()
-    n_parts = int(sum((int(c) + pt - 1) // pt for c in cap))  # partitions of the batch
+    n_parts = dec.partitions_total(len(cap))  # partitions of the batch
     row = D // 32 * 34
     kv = int(cap.sum()) * Hkv * 2 * row
     qo = B * q_len * Hq * D * (2 + 4)

@@ -825,23 +825,33 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
     return e < p.batch ? entry_len(p, sq) : -1;
   };
   const int n_chunks = (p.batch + 63) / 64;
+  // Partitions of a length-L entry at partition length t: ceil(L / t), less
+  // one when the last would hold at most one tile and the one before can
+  // take it within 64 pages (device-chosen lengths only: the per-entry
+  // layout of an explicit length counts ceil(L / t)).  An entry that grew
+  // by this step's token past a multiple of t so keeps its partition count.
+  const bool merge = p.part_tokens == 0;
+  auto parts = [&](int32_t L, int32_t t) -> int32_t {
+    if (L <= 0) return L < 0 ? 0 : 1;
+    int32_t n = (L + t - 1) / t;
+    if (merge && n > 1 && L - (n - 1) * t <= kTile && t + kTile <= 64 * p.g.page_tokens) --n;
+    return n;
+  };
   pt = p.part_tokens;
   if (pt == 0) {
     int32_t sq;
     auto count = [&](int32_t t) -> int32_t {
       int32_t tot = 0;
-      for (int c = 0; c < n_chunks; ++c) {
-        const int32_t L = len_at(c, sq);
-        tot += wave_isum(L < 0 ? 0 : (L > 0 ? (L + t - 1) / t : 1), lane);
-      }
+      for (int c = 0; c < n_chunks; ++c) tot += wave_isum(parts(len_at(c, sq), t), lane);
       return tot;
     };
-    // count(k*unit) >= (sum of ceil(L/unit)) / k, so no k below
-    // ceil(that sum / target) can do: start the search there (exact in one
-    // evaluation when the lengths are equal)
+    // count(k*unit) >= (sum of ceil((L - kTile)/unit)) / k (a merge drops at
+    // most one tile of an entry), so no k below ceil(that sum / target) can
+    // do: start the search there (exact in one evaluation when the lengths
+    // are equal)
     int32_t units = 0;
     for (int c = 0; c < n_chunks; ++c) {
-      const int32_t L = len_at(c, sq);
+      const int32_t L = len_at(c, sq) - kTile;
       units += wave_isum(L > 0 ? (L + p.pt_unit - 1) / p.pt_unit : 0, lane);
     }
     const int32_t k0 = (units + p.target_parts - 1) / p.target_parts;
@@ -864,7 +874,7 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
   for (int c = 0; c < n_chunks; ++c) {
     int32_t sq;
     const int32_t L = len_at(c, sq);
-    const int32_t n = L < 0 ? 0 : (L > 0 ? (L + pt - 1) / pt : 1);
+    const int32_t n = parts(L, pt);
     const int32_t cum = wave_iscan(n, lane);
     const uint64_t hit = __ballot(L >= 0 && base + cum > x);
     if (hit != 0) {
@@ -931,7 +941,7 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     return;
   }
   const int32_t tok0 = part * pt;
-  const int32_t tok_end = min(len, tok0 + pt);
+  const int32_t tok_end = part == nb - 1 ? len : min(len, tok0 + pt);  // the last takes the rest
   dc.b = b;
   dc.seq = seq;
   dc.len = len;
