@@ -580,19 +580,23 @@ WsLayout ws_layout(const rkv_kv_geometry *g, const rkv_decode_args *a, const Pla
     n_entry = std::min(n_entry, std::max(by_target, (pl.max_len + longest - 1) / longest));
   }
   n_entry = std::min<int64_t>(n_entry, pl.n_wg);
-  // Combine splits: enough (row, entry, split) blocks to keep ~256 CUs busy
-  // when the batch has few rows, else one split per row; a split holds at
-  // least 16 partitions.
+  // Combine splits: up to 256 (row, entry, split) blocks to keep the CUs
+  // busy when the batch has few rows, else one split per row; a split holds
+  // at least 16 partitions.  rows * splits <= max(rows, 256), and the split
+  // area is reserved at that bound, so every part of the layout grows with
+  // batch and max_seq_len: a workspace sized for the largest call of a
+  // serving loop holds every smaller one.
   const int64_t blocks = std::max<int64_t>(1, (int64_t)out_rows);
-  const int64_t want = std::max<int64_t>(1, (256 + blocks - 1) / blocks);
+  const int64_t want = std::max<int64_t>(1, 256 / blocks);
   const int64_t max_splits = std::max<int64_t>(1, (n_entry + 15) / 16);
   w.splits = (int32_t)std::min(want, max_splits);
   w.chunk = (int32_t)std::max<int64_t>(1, (n_entry + w.splits - 1) / w.splits);
+  const size_t split_rows = std::max<size_t>(out_rows, 256);
   w.ml = align256(sizeof(int32_t) * (1 + 2 * B));
   w.o = w.ml + align256(sizeof(float) * 2 * prows);
   w.sml = w.o + align256(sizeof(float) * prows * g->head_dim);
-  w.so = w.sml + align256(sizeof(float) * 2 * out_rows * w.splits);
-  w.total = w.so + sizeof(float) * out_rows * w.splits * g->head_dim;
+  w.so = w.sml + align256(sizeof(float) * 2 * split_rows);
+  w.total = w.so + sizeof(float) * split_rows * g->head_dim;
   return w;
 }
 size_t ws_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a, const Plan &pl) {
@@ -1264,13 +1268,15 @@ struct rkv_pool {
   size_t layer_bytes = 0;
   int32_t *d_tables = nullptr;
   int32_t *d_lens = nullptr;
-  // table uploads: two pinned host staging buffers (reused every other
-  // sync, after the event of their last copy) and one device buffer, all of
-  // the packed size max_seqs * (W + 1) + max_seqs int32
-  // ... followed by room for num_pages queued copy-on-write pairs
+  // table uploads: two slots, each a pinned host staging buffer and a device
+  // buffer of the packed size max_seqs * (W + 1) + max_seqs int32, followed
+  // by room for num_pages queued copy-on-write pairs.  A slot is reused every
+  // other sync, after the event recorded behind the last kernel that read its
+  // device buffer, so syncs on different streams never overwrite a buffer
+  // still in use.
   int32_t *h_stage[2] = {nullptr, nullptr};
   hipEvent_t stage_done[2] = {nullptr, nullptr};
-  int32_t *d_stage = nullptr;
+  int32_t *d_stage[2] = {nullptr, nullptr};
   uint32_t n_syncs = 0;
   // R4KV page CRC: device result word and its pinned host copy
   uint32_t *d_crc = nullptr;
@@ -1328,7 +1334,8 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
        (e = hipMalloc(&p->pages, all_pages)) != hipSuccess) ||
       (e = hipMalloc(&p->d_tables, tbytes)) != hipSuccess ||
       (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess ||
-      (e = hipMalloc(&p->d_stage, sbytes)) != hipSuccess ||
+      (e = hipMalloc(&p->d_stage[0], sbytes)) != hipSuccess ||
+      (e = hipMalloc(&p->d_stage[1], sbytes)) != hipSuccess ||
       (e = hipHostMalloc(&p->h_stage[0], sbytes, hipHostMallocDefault)) != hipSuccess ||
       (e = hipHostMalloc(&p->h_stage[1], sbytes, hipHostMallocDefault)) != hipSuccess ||
       (e = hipEventCreateWithFlags(&p->stage_done[0], hipEventDisableTiming)) != hipSuccess ||
@@ -1367,7 +1374,8 @@ rkv_status rkv_pool_destroy(rkv_pool *p) {
   else (void)hipFree(p->pages);
   (void)hipFree(p->d_tables);
   (void)hipFree(p->d_lens);
-  (void)hipFree(p->d_stage);
+  (void)hipFree(p->d_stage[0]);
+  (void)hipFree(p->d_stage[1]);
   (void)hipFree(p->d_crc);
   if (p->h_crc) (void)hipHostFree(p->h_crc);
   for (int i = 0; i < 2; ++i) {
@@ -1390,7 +1398,7 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   // one transfer, then the page copies run and the rows are scattered on the
   // device, so launches queued after this call on `stream` see the new
   // tables and copied pages, and earlier ones the old.  Nothing here waits
-  // for the device unless the staging buffer's copy from two syncs ago is
+  // for the device unless the staging slot's kernels from two syncs ago are
   // still pending.
   rkv_alloc *a = p->alloc;
   const int32_t W = a->d.max_pages_per_seq;
@@ -1414,17 +1422,18 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   if (rkv_status s = rkv_alloc_take_copies(a, h + pairs_at, a->d.num_pages, &n_pairs)) return s;
   const size_t bytes = sizeof(int32_t) * (pairs_at + 2 * (size_t)n_pairs);
   hipStream_t hs = as_stream(stream);
-  if ((e = hipMemcpyAsync(p->d_stage, h, bytes, hipMemcpyHostToDevice, hs)) != hipSuccess)
+  int32_t *d = p->d_stage[slot];
+  if ((e = hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, hs)) != hipSuccess)
     return hip_fail(op, e);
-  if ((e = hipEventRecord(p->stage_done[slot], hs)) != hipSuccess) return hip_fail(op, e);
   ++p->n_syncs;
   if ((e = rkv::launch_copy_pages(p->pages, (int64_t)p->layer_bytes, p->d.layers, p->d.num_pages,
-                                  p->d_stage + pairs_at, n_pairs,
+                                  d + pairs_at, n_pairs,
                                   (int64_t)rkv::page_bytes(to_geo(&p->g)), hs)) != hipSuccess)
     return hip_fail(op, e);
-  if ((e = rkv::launch_table_scatter(p->d_stage, n_rows, W, S, p->d_tables, p->d_lens, hs)) !=
-      hipSuccess)
+  if ((e = rkv::launch_table_scatter(d, n_rows, W, S, p->d_tables, p->d_lens, hs)) != hipSuccess)
     return hip_fail(op, e);
+  // the slot's host and device buffers are free again once this has run
+  if ((e = hipEventRecord(p->stage_done[slot], hs)) != hipSuccess) return hip_fail(op, e);
   return RKV_OK;
 }
 

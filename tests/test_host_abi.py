@@ -131,3 +131,38 @@ def test_allocator_errors(rkv):
         a.reserve(0, 30)  # shrinking through reserve is refused
     assert e.value.status == rkv.ERR_INVALID_ARG
     assert "rkv_seq_reserve" in rkv.lib().rkv_last_error().decode()
+
+
+def _ws(rkv, g, B, L, q_heads, q_len=1, pt=0):
+    a = rkv.DecodeArgs(B, None, None, rkv.BF16, q_len, q_heads, 1.0, None, rkv.F32, pt, L, None, 0,
+                       None, None)
+    return rkv.decode_workspace_bytes(g, a)
+
+
+@pytest.mark.parametrize("kv_heads,q_heads,D,PT,max_decode,max_len", [
+    (8, 32, 128, 16, 8, 16384),   # the advisor's case: 3..7 rows refused before
+    (8, 64, 128, 16, 4, 8192),
+    (2, 16, 256, 64, 64, 65536),
+    (2, 16, 256, 64, 16, 262144),
+    (1, 1, 128, 32, 40, 4096),
+])
+def test_decode_workspace_monotone(rkv, kv_heads, q_heads, D, PT, max_decode, max_len):
+    """A workspace sized for the largest call (max_decode entries of the
+    longest length) holds every smaller call: the serving adapter allocates it
+    once (rkv_serve_create)."""
+    g = rkv.geometry(kv_heads, D, PT, 1 << 20)
+    top = _ws(rkv, g, max_decode, max_len, q_heads)
+    lens = sorted({1, PT, 256, 257, 1000, 4096, 4097, max_len // 3, max_len - 1, max_len})
+    prev_b = 0
+    for B in range(1, max_decode + 1):
+        prev_l = 0
+        for L in lens:
+            if L > max_len:
+                continue
+            w = _ws(rkv, g, B, L, q_heads)
+            assert w <= top, (B, L, w, top)
+            assert w >= prev_l, ("not monotone in length", B, L)
+            prev_l = w
+        w_top = _ws(rkv, g, B, max_len, q_heads)
+        assert w_top >= prev_b, ("not monotone in batch", B)
+        prev_b = w_top
