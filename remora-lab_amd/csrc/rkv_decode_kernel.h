@@ -21,12 +21,15 @@
 //             lane, 1 KiB per instruction, fully coalesced), NSTAGE deep.
 //   QK      : S^T[token][row] on v_mfma_i32_16x16x64_i8.  A = K codes (int8,
 //             exactly the stored bytes, no dequant), B = the query split
-//             into two int8 planes q ~ sq*(128*hi + lo).  The B operand's 16
-//             columns are 8 rows x 2 block parities: columns 0-7 carry the
-//             even 32-dim block of the 64-dim step, columns 8-15 the odd
-//             one, so every int32 result is one (token, row, Q8 block) dot
-//             product and gets its own f16 K scale on the VALU (exact
-//             dequant order: d_k * sum(q_int * k_int)).
+//             into three int8 planes q ~ sq*(128*hi + md + lo/128) (22
+//             significant bits per row).  The B operand's 16 columns are 8
+//             rows x 2 block parities: columns 0-7 carry the even 32-dim
+//             block of the 64-dim step, columns 8-15 the odd one, so every
+//             int32 result is one (token, row, Q8 block) dot product and
+//             gets its own f16 K scale on the VALU (exact dequant order:
+//             d_k * sum(q_int * k_int)).  The lo plane's dot, shifted right
+//             by 7, is the accumulator input of the md plane's MFMA, so the
+//             third plane costs one MFMA and one shift per result.
 //   softmax : scores live one row per lane column; max across the 4 lane
 //             groups with two shuffles, exp2 on the VALU.
 //   PV      : O^T[dim][row] on v_mfma_f32_16x16x32_f16.  A = V codes
@@ -35,6 +38,8 @@
 //             scale of that token and block) as two f16 terms; f32
 //             accumulation.
 #pragma once
+
+#include <type_traits>
 
 #include "rkv_launch.h"
 
@@ -258,6 +263,15 @@ struct Decoder {
   static constexpr int NP = (NT + 1) / 2;  // PV n-tiles of 16 rows
   static constexpr int NC = D / 64;        // 64-dim QK steps
   static constexpr int NB = D / 32;        // Q8 blocks per row
+  // 16 rows per wave (NT == 2): the QK runs on v_mfma_i32_16x16x32_i8, one
+  // Q8 block per MFMA with the wave's 16 rows in its 16 columns, so each
+  // lane's int32 result is a whole (token, row, block) dot and the query
+  // operands hold no zero half (8 bytes per block and plane).  With at most
+  // 8 rows the 16x16x64 form packs 8 rows x 2 block parities instead.
+  static constexpr bool kWide = NT == 2;
+  using QOp = typename std::conditional<kWide, int64_t, v4i>::type;
+  static constexpr int kQR = kWide ? 1 : NT;   // query operand sets
+  static constexpr int kQC = kWide ? NB : NC;  // operands per set and plane
 
   const DecodeLaunch &p;
   int lane, li, lg, kvh, b, wave;
@@ -270,8 +284,8 @@ struct Decoder {
   const uint8_t *kv_base;  // pages + kv head offset
   uint64_t PB;
   ChunkPlan<D, kSmall, kKReg> plan;
-  v4i kreg[2][D / 64];     // kKReg: K codes of the tile being computed (A operands)
-  v4i qhi[NT][NC], qlo[NT][NC];
+  QOp kreg[2][kQC];        // kKReg: K codes of the tile being computed (A operands)
+  QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
   float rmul[NP];
   int32_t rlim[NP];
   v4f oacc[NP][D / 16];
@@ -355,19 +369,21 @@ struct Decoder {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  // kKReg: K codes of tile `tile` into kreg.  Lane (li, lg) of M-tile mt,
-  // 64-dim step c holds token row 16*mt + li, dims 64*c + 16*lg .. +15.
+  // kKReg: K codes of tile `tile` into kreg.  Lane (li, lg) of M-tile mt
+  // holds token row 16*mt + li: dims 64*c + 16*lg .. +15 of 64-dim step c,
+  // or (kWide) dims 32*blk + 8*lg .. +7 of block blk.
   __device__ __forceinline__ void load_k(int tile) {
     const Geo &g = p.g;
     const int32_t t0 = tok0 + tile * kTile;
     const int32_t pid = __builtin_amdgcn_readlane(pidv, t0 / g.page_tokens - pg_first);
     const uint8_t *base = kv_base + (uint64_t)pid * PB +
-                          (uint64_t)((t0 % g.page_tokens) + li) * D + 16 * lg;
+                          (uint64_t)((t0 % g.page_tokens) + li) * D + (kWide ? 8 : 16) * lg;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        kreg[mt][c] = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(base + (uint64_t)(16 * mt) * D + 64 * c));
+      for (int c = 0; c < kQC; ++c)
+        kreg[mt][c] = __builtin_nontemporal_load(
+            reinterpret_cast<const QOp *>(base + (uint64_t)(16 * mt) * D + (kWide ? 32 : 64) * c));
   }
 
   // Scores, online softmax and PV for the tile held in LDS stage `st`
@@ -375,33 +391,64 @@ struct Decoder {
   __device__ __forceinline__ void compute(int tile, const lds_u8 *st, lds_u8 *next_stage = nullptr) {
     const int32_t t0 = tok0 + tile * kTile;
     // ---- QK^T: int32 block dots, scaled by the f16 K scale of (token, block) ----
-    float sacc[NT][2][4];
+    // Each plane set computes t = 128*dot(hi) + dot(md) + floor(dot(lo)/128):
+    // the lo plane's dot, shifted, is the accumulator input of the md
+    // plane's MFMA.  |t| < 2^27, so every step is exact in int32 and the f32
+    // conversion rounds once.
+    float sacc[kQR][2][4];
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
+    for (int nt = 0; nt < kQR; ++nt)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sacc[nt][mt][r] = 0.0f;
+    if constexpr (kWide) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int krow = 16 * mt + li;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const int pc = (4 * c + lg) ^ (krow & (S::kCPR - 1));
-        const v4i a = kKReg ? kreg[mt][c] : lds_load<v4i>(st + S::kKC + krow * D + 16 * pc);
-        const int blk = 2 * c + (li >> 3);
+      for (int blk = 0; blk < NB; ++blk) {
         // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
         const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
-        const float dk[4] = {(float)dk8[4 * mt], (float)dk8[4 * mt + 1], (float)dk8[4 * mt + 2],
-                             (float)dk8[4 * mt + 3]};
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
+        for (int mt = 0; mt < 2; ++mt) {
+          const int krow = 16 * mt + li;
+          // dims 32*blk + 8*lg .. +7: half (lg & 1) of logical 16-byte chunk 2*blk + (lg >> 1)
+          const int pc = (2 * blk + (lg >> 1)) ^ (krow & (S::kCPR - 1));
+          const int64_t a = kKReg ? kreg[mt][blk]
+                                  : lds_load<int64_t>(st + S::kKC + krow * D + 16 * pc + 8 * (lg & 1));
           const v4i z = {0, 0, 0, 0};
-          const v4i ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[nt][c], z, 0, 0, 0);
-          const v4i cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[nt][c], z, 0, 0, 0);
+          const v4i cl = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, qlo[0][blk], z, 0, 0, 0);
+          const v4i cls = {cl[0] >> 7, cl[1] >> 7, cl[2] >> 7, cl[3] >> 7};
+          const v4i cm = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, qmd[0][blk], cls, 0, 0, 0);
+          const v4i ch = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, qhi[0][blk], z, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            sacc[nt][mt][r] = __builtin_fmaf((float)((ch[r] << 7) + cl[r]), dk[r], sacc[nt][mt][r]);
+            sacc[0][mt][r] = __builtin_fmaf((float)((ch[r] << 7) + cm[r]), (float)dk8[4 * mt + r],
+                                            sacc[0][mt][r]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int krow = 16 * mt + li;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          const int pc = (4 * c + lg) ^ (krow & (S::kCPR - 1));
+          const v4i a = kKReg ? kreg[mt][c] : lds_load<v4i>(st + S::kKC + krow * D + 16 * pc);
+          const int blk = 2 * c + (li >> 3);
+          // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
+          const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
+          const float dk[4] = {(float)dk8[4 * mt], (float)dk8[4 * mt + 1], (float)dk8[4 * mt + 2],
+                               (float)dk8[4 * mt + 3]};
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            const v4i z = {0, 0, 0, 0};
+            const v4i cl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qlo[nt][c], z, 0, 0, 0);
+            const v4i cls = {cl[0] >> 7, cl[1] >> 7, cl[2] >> 7, cl[3] >> 7};
+            const v4i cm = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qmd[nt][c], cls, 0, 0, 0);
+            const v4i ch = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, qhi[nt][c], z, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              sacc[nt][mt][r] = __builtin_fmaf((float)((ch[r] << 7) + cm[r]), dk[r], sacc[nt][mt][r]);
+          }
         }
       }
     }
@@ -431,17 +478,22 @@ struct Decoder {
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          // the even- and odd-block halves of a row sit 8 columns apart
-          float lo_t = 0.f, hi_t = 0.f;
+          float v;
+          if constexpr (kWide) {
+            v = sacc[0][mt][r] * rmul[np];
+          } else {
+            // the even- and odd-block halves of a row sit 8 columns apart
+            float lo_t = 0.f, hi_t = 0.f;
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            if (nt != 2 * np && nt != 2 * np + 1) continue;
-            const float tot = sacc[nt][mt][r] + dpp_ror8(sacc[nt][mt][r]);
-            if (nt == 2 * np) lo_t = tot;
-            else hi_t = tot;
+            for (int nt = 0; nt < NT; ++nt) {
+              if (nt != 2 * np && nt != 2 * np + 1) continue;
+              const float tot = sacc[nt][mt][r] + dpp_ror8(sacc[nt][mt][r]);
+              if (nt == 2 * np) lo_t = tot;
+              else hi_t = tot;
+            }
+            // kColSplit: lanes li >= 8 hold row li - 8 (the ror-8 sum is symmetric)
+            v = (kColSplit || li < 8 ? lo_t : hi_t) * rmul[np];
           }
-          // kColSplit: lanes li >= 8 hold row li - 8 (the ror-8 sum is symmetric)
-          const float v = (kColSplit || li < 8 ? lo_t : hi_t) * rmul[np];
           const int tok = t0 + 16 * mt + 4 * lg + r;
           const float sv = tok < rlim[np] ? v : -INFINITY;
           s[4 * mt + r] = sv;
@@ -675,12 +727,30 @@ struct Decoder {
 // whose D values start at element `qbase` of q (qbase < 0: a dead row, all
 // zeros), dims 64*c + 16*lg .. +15.  It is live for the even block (lg < 2)
 // when li < 8 and for the odd block (lg >= 2) when li >= 8.  The row is
-// split into two int8 planes, q ~ sq * (128*hi + lo), and `qmul` returns
+// split into three int8 planes, q ~ sq * (128*hi + md + lo/128) with
+// sq = amax/16256: u = q/sq is rounded to the integer Q = 128*hi + md
+// (|hi| <= 127, md in [-64, 63]) and its remainder u - Q (exact in f32) to
+// lo/128 (|lo| <= 64).  Each element is then within sq/256 = amax*2^-22 of
+// q: a bf16 q is exact when its exponent is within 13 of the row maximum's,
+// and outlier channels (amax >> typical |q|) leave the other elements
+// 2^7 times finer than a two-plane split would.  `qmul` returns
 // sq * scale_log2 (the same on every lane of the row).
+// Bytes of the three planes of one query element, u = q / sq (|u| <= 16256).
+__device__ __forceinline__ void q_split(float u, uint32_t &hi8, uint32_t &md8, uint32_t &lo8) {
+  const float r = fminf(fmaxf(rintf(u), -16256.0f), 16256.0f);
+  const int32_t Q = (int32_t)r;
+  const int32_t hi = (Q + 64) >> 7;
+  const int32_t md = Q - 128 * hi;
+  const int32_t lo = max(-127, min(127, (int32_t)rintf((u - r) * 128.0f)));
+  hi8 = (uint32_t)(uint8_t)(int8_t)hi;
+  md8 = (uint32_t)(uint8_t)(int8_t)md;
+  lo8 = (uint32_t)(uint8_t)(int8_t)lo;
+}
+
 template <int D>
 __device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t qbase, int li,
-                                              int lg, float scale_log2, v4i *qhi, v4i *qlo,
-                                              float &qmul) {
+                                              int lg, float scale_log2, v4i *qhi, v4i *qmd,
+                                              v4i *qlo, float &qmul) {
   constexpr int NC = D / 64;
   float qv[NC][16];
 #pragma unroll
@@ -723,25 +793,91 @@ __device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t
     for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
   amax = fmaxf(amax, __shfl_xor(amax, 16));
   amax = fmaxf(amax, __shfl_xor(amax, 32));
-  // q ~ sq * Q with |Q| <= 16256 = 127*128; Q = 128*hi + lo with hi in
-  // [-127, 127] and lo in [-64, 63].
   const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
   qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
   const bool live = (li < 8) == (lg < 2);
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    uint32_t hw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+    uint32_t hw[4] = {0, 0, 0, 0}, mw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      int32_t Q = (int32_t)rintf(qv[c][e] * inv);
-      Q = live ? max(-16256, min(16256, Q)) : 0;
-      const int32_t hi = (Q + 64) >> 7;
-      const int32_t lo = Q - 128 * hi;
-      hw[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)hi) << (8 * (e & 3));
-      lw[e >> 2] |= ((uint32_t)(uint8_t)(int8_t)lo) << (8 * (e & 3));
+      uint32_t h8, m8, l8;
+      q_split(live ? qv[c][e] * inv : 0.0f, h8, m8, l8);
+      hw[e >> 2] |= h8 << (8 * (e & 3));
+      mw[e >> 2] |= m8 << (8 * (e & 3));
+      lw[e >> 2] |= l8 << (8 * (e & 3));
     }
     qhi[c] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
+    qmd[c] = v4i{(int)mw[0], (int)mw[1], (int)mw[2], (int)mw[3]};
     qlo[c] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+  }
+}
+
+// The query operands of the 16-row QK (Decoder::kWide): lane (li, lg) holds
+// row li's dims 32*blk + 8*lg .. +7 of every block blk, as the B operand of
+// v_mfma_i32_16x16x32_i8 (k = 8*lg .. 8*lg+7, column li); qbase < 0 is a
+// dead row (zeros).  Same planes and `qmul` as load_q_planes.
+template <int D>
+__device__ __forceinline__ void load_q_wide(const void *qp, bool bf16, int64_t qbase, int lg,
+                                            float scale_log2, int64_t *qhi, int64_t *qmd,
+                                            int64_t *qlo, float &qmul) {
+  constexpr int NB = D / 32;
+  float qv[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[b][e] = 0.0f;
+  if (qbase >= 0) {
+    const int64_t base = qbase + 8 * lg;
+    if (bf16) {
+      const uint16_t *q = static_cast<const uint16_t *>(qp) + base;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint4 w = *reinterpret_cast<const uint4 *>(q + 32 * b);
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[b][2 * e] = bf16_bits_to_f32((uint16_t)(ws[e] & 0xffffu));
+          qv[b][2 * e + 1] = bf16_bits_to_f32((uint16_t)(ws[e] >> 16));
+        }
+      }
+    } else {
+      const float *q = static_cast<const float *>(qp) + base;
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e4 = 0; e4 < 2; ++e4) {
+          const float4 w = *reinterpret_cast<const float4 *>(q + 32 * b + 4 * e4);
+          qv[b][4 * e4] = w.x;
+          qv[b][4 * e4 + 1] = w.y;
+          qv[b][4 * e4 + 2] = w.z;
+          qv[b][4 * e4 + 3] = w.w;
+        }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[b][e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
+  qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    uint64_t h = 0, m = 0, l = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint32_t h8, m8, l8;
+      q_split(qv[b][e] * inv, h8, m8, l8);
+      h |= (uint64_t)h8 << (8 * e);
+      m |= (uint64_t)m8 << (8 * e);
+      l |= (uint64_t)l8 << (8 * e);
+    }
+    qhi[b] = (int64_t)h;
+    qmd[b] = (int64_t)m;
+    qlo[b] = (int64_t)l;
   }
 }
 
@@ -971,20 +1107,25 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   const int32_t q_per_kv = p.q_heads / g.kv_heads;
   const int32_t R = p.q_len * q_per_kv;
 
-  // ---- query: int8 hi/lo planes as MFMA B operands -------------------------
-  // Lane (li, lg) of QK n-tile nt serves row 8*nt + (li & 7) of this wave.
+  // ---- query: int8 hi/md/lo planes as MFMA B operands ----------------------
+  // Lane (li, lg) of QK n-tile nt serves row 8*nt + (li & 7) of this wave;
+  // with Dec::kWide it serves row li.  qrow(row) is the row's first element
+  // in q, or -1 past the last row.
+  auto qrow = [&](int row) -> int64_t {
+    if (row >= R) return -1;
+    const int j = row / q_per_kv;
+    const int h = kvh * q_per_kv + row % q_per_kv;
+    return (((int64_t)b * p.q_len + j) * p.q_heads + h) * D;
+  };
   float qmul[NT];
+  if constexpr (Dec::kWide) {
+    load_q_wide<D>(p.q, p.q_bf16 != 0, qrow(r0 + li), lg, p.scale_log2, dc.qhi[0], dc.qmd[0],
+                   dc.qlo[0], qmul[0]);
+  } else {
 #pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int row = r0 + 8 * nt + (li & 7);
-    int64_t qbase = -1;
-    if (row < R) {
-      const int j = row / q_per_kv;
-      const int h = kvh * q_per_kv + row % q_per_kv;
-      qbase = (((int64_t)b * p.q_len + j) * p.q_heads + h) * D;
-    }
-    load_q_planes<D>(p.q, p.q_bf16 != 0, qbase, li, lg, p.scale_log2, dc.qhi[nt], dc.qlo[nt],
-                     qmul[nt]);
+    for (int nt = 0; nt < NT; ++nt)
+      load_q_planes<D>(p.q, p.q_bf16 != 0, qrow(r0 + 8 * nt + (li & 7)), li, lg, p.scale_log2,
+                       dc.qhi[nt], dc.qmd[nt], dc.qlo[nt], qmul[nt]);
   }
 
   // ---- per-lane softmax rows: PV n-tile np, column li -> row 16*np + li ---
@@ -994,10 +1135,15 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     const int row = r0 + 16 * np + (Dec::kColSplit ? (li & 7) : li);
     const int nt = Dec::kColSplit ? 0 : 2 * np + (li >> 3);
     // every lane of column li computed the scale of row 8*nt + (li & 7)
+    // (kWide: of row li itself)
     float mul = 0.0f;
+    if constexpr (Dec::kWide) {
+      mul = qmul[0];
+    } else {
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
-      if (t == nt) mul = qmul[t];
+      for (int t = 0; t < NT; ++t)
+        if (t == nt) mul = qmul[t];
+    }
     dc.rmul[np] = mul;
     dc.rlim[np] = (row < R && nt < NT) ? len - p.q_len + row / q_per_kv + 1 : 0;
     dc.mref[np] = -INFINITY;

@@ -112,22 +112,16 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.vf16 = (lds_u8 *)v_f16;
 
   const int32_t G = p.q_heads / g.kv_heads;  // rows of one chunk token
-  // row r of the block: chunk token j0 + r / G, q head kvh*G + r % G
-  float qmul[2];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int r = r0 + 8 * nt + (li & 7);
-    const int jl = r / G;
-    int64_t qbase = -1;
-    if (jl < jn)
-      qbase = ((int64_t)(pf.qoff[e] + j0 + jl) * p.q_heads + kvh * G + r % G) * D;
-    load_q_planes<D>(p.q, p.q_bf16 != 0, qbase, li, lg, p.scale_log2, dc.qhi[nt], dc.qlo[nt],
-                     qmul[nt]);
-  }
+  // row r of the block: chunk token j0 + r / G, q head kvh*G + r % G; the
+  // wave's 16 rows take the 16x16x32 QK (Dec::kWide), lane (li, lg) row r0 + li
+  static_assert(Dec::kWide, "prefill waves hold 16 rows");
   {
-    const int r = r0 + li;  // softmax row of this lane (PV n-tile 0, column li)
+    const int r = r0 + li;  // query and softmax row of this lane (PV n-tile 0, column li)
     const int jl = r / G;
-    dc.rmul[0] = li < 8 ? qmul[0] : qmul[1];
+    const int64_t qbase =
+        jl < jn ? ((int64_t)(pf.qoff[e] + j0 + jl) * p.q_heads + kvh * G + r % G) * D : -1;
+    load_q_wide<D>(p.q, p.q_bf16 != 0, qbase, lg, p.scale_log2, dc.qhi[0], dc.qmd[0], dc.qlo[0],
+                   dc.rmul[0]);
     dc.rlim[0] = jl < jn ? ctx + j0 + jl + 1 : 0;
     dc.mref[0] = -INFINITY;
     dc.lrun[0] = 0.0f;

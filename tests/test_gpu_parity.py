@@ -181,6 +181,66 @@ def test_append_bitexact(rkv, rko, ctx, D, PT, rule, bf16):
                 assert np.array_equal(got[h], want), f"seq {b} kind {kind} head {h}"
 
 
+@pytest.mark.parametrize("D,PT,order", [
+    (256, 64, "chunks"), (256, 64, "shuffled"), (128, 16, "interleaved"), (256, 32, "bad_rows"),
+    (128, 128, "chunks"), (256, 16, "shuffled")])
+def test_append_row_orders(rkv, rko, ctx, D, PT, order):
+    """The append kernel quantizes 32 input rows per workgroup and writes 4
+    aligned consecutive slots of a page with one store: the page bytes equal
+    the oracle's for rows in any order -- chunks starting mid-tile, shuffled
+    rows, two sequences interleaved row by row, and invalid rows inside a
+    group (reported, nothing written for them)."""
+    torch = _torch()
+    Hkv = 2
+    rng = np.random.default_rng(D + PT + len(order))
+    lens = [700, 413, 97]
+    npg = [(L + PT - 1) // PT for L in lens]
+    num_pages = sum(npg) + 5
+    perm = rng.permutation(num_pages).astype(np.int32)
+    W = max(npg)
+    bt = np.full((3, W), -1, np.int32)
+    o = 0
+    for b in range(3):
+        bt[b, :npg[b]] = perm[o:o + npg[b]]
+        o += npg[b]
+    sid = np.concatenate([np.full(L, b, np.int32) for b, L in enumerate(lens)])
+    pos = np.concatenate([np.arange(L, dtype=np.int32) for L in lens])
+    if order == "chunks":      # prefill-like chunks starting at unaligned positions
+        cuts = [0, 13, 77, 300, 301, 700, 700 + 5, 700 + 413, len(sid)]
+        idx = np.concatenate([np.arange(cuts[i], cuts[i + 1]) for i in rng.permutation(len(cuts) - 1)])
+    elif order == "interleaved":
+        a, b2 = np.arange(0, 413), np.arange(700, 700 + 413)
+        idx = np.concatenate([np.stack([a, b2], 1).reshape(-1), np.arange(413, 700),
+                              np.arange(1113, len(sid))])
+    else:
+        idx = rng.permutation(len(sid)) if order == "shuffled" else np.arange(len(sid))
+    sid, pos = sid[idx], pos[idx]
+    k = rng.standard_normal((len(sid), Hkv, D)).astype(np.float32)
+    v = rng.standard_normal((len(sid), Hkv, D)).astype(np.float32)
+    bad = np.zeros(len(sid), bool)
+    if order == "bad_rows":    # a bad sequence id, a position past the table, a -1 page
+        bad[[5, 40, 41, 100]] = True
+        sid[5] = 7
+        pos[40] = W * PT + 3
+        pos[41] = -1
+        bt[2, npg[2] - 1] = -1
+        bad |= (sid == 2) & (pos // PT == npg[2] - 1)
+    g = rkv.geometry(Hkv, D, PT, num_pages)
+    lay = rko.layout(Hkv, D, PT, num_pages)
+    want = np.zeros(num_pages * rkv.page_bytes(g), np.uint8)
+    rko.paged_append(lay, want, bt, sid[~bad], pos[~bad], k[~bad], v[~bad], 0)
+    pages = torch.zeros(want.size, dtype=torch.uint8, device="cuda")
+    rkv.append_q8(ctx, g, pages, torch.from_numpy(bt).cuda(), torch.from_numpy(sid).cuda(),
+                  torch.from_numpy(pos).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+    if bad.any():
+        with pytest.raises(rkv.RkvError) as e:
+            ctx.sync()
+        assert e.value.status == rkv.ERR_BAD_BLOCK_TABLE
+    ctx.sync()
+    got = pages.cpu().numpy()
+    assert np.array_equal(got, want), f"{int(np.sum(got != want))} page bytes differ"
+
+
 def test_append_special_values(rkv, rko, ctx):
     """Zero blocks, huge (f16-overflowing scale), tiny (subnormal scale), inf and
     NaN inputs quantize identically on both sides, for both rules."""
@@ -298,6 +358,49 @@ def test_decode_ragged_device_partitions(rkv, rko, ctx, Hq, Hkv, D, PT, lens):
     want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(len(lens), dtype=np.int32),
                             q, 1.0 / math.sqrt(D), pt)
     assert_close(got, want, what="ragged")
+
+
+def outlier_q(rng, shape):
+    """q ~ N(0,1) whose every head carries ceil(1% of D) channels scaled x32
+    and one more channel scaled x100: queries after RoPE concentrate their
+    energy in a few channels, so a row's largest |q| is 30-100x its typical
+    element."""
+    q = rng.standard_normal(shape).astype(np.float32)
+    H, D = shape[-2], shape[-1]
+    n32 = max(1, int(math.ceil(0.01 * D)))
+    for h in range(H):
+        ch = rng.choice(D, n32 + 1, replace=False)
+        q[..., h, ch[:n32]] *= 32.0
+        q[..., h, ch[n32]] *= 100.0
+    return q
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,PT,lens,q_bf16,q_len", [
+    # 8 rows per kv head: the 16x16x64 QK (8 rows x 2 block parities)
+    (16, 2, 256, 64, [4100, 700, 33, 1, 2000], True, 1),
+    (16, 2, 256, 64, [3000, 9, 1500], False, 1),
+    (8, 2, 128, 16, [700, 3, 2048], False, 1),
+    # 16 rows: the 16x16x32 QK on one wave
+    (32, 2, 256, 64, [2500, 40, 1000], True, 1),
+    (16, 2, 128, 32, [1200, 64], True, 2),
+    # 32 rows: the two-wave causal verify
+    (16, 2, 256, 64, [1504, 74, 37], True, 4),
+])
+def test_decode_outlier_query(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_bf16, q_len):
+    """Queries with outlier channels (x32 and x100) against the reference's
+    f32 q (attention.rs:186-192), at the same bars: the query's int8 planes
+    must resolve the small elements of a row next to its outliers."""
+    print(f"outlier q Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens} q_len={q_len}", flush=True)
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=3 * Hq + D + q_len, outliers=0.01, src_bf16=True)
+    rng = np.random.default_rng(D + Hq + q_len)
+    q = outlier_q(rng, (len(lens), q_len, Hq, D))
+    if q_bf16:
+        q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    scale = 1.0 / math.sqrt(D)
+    got, pt = _run_decode(rkv, ctx, sc, q, scale, q_bf16=q_bf16, q_len=q_len)
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(len(lens), dtype=np.int32),
+                            q, scale, pt)
+    assert_close(got, want, what=f"outlier q rows={q_len * Hq // Hkv} pt={pt}")
 
 
 def test_smoke_mirror(rkv, rko, ctx):

@@ -10,7 +10,8 @@ len - q_len + j + 1 positions).  Bars as in test_gpu_parity.py: max-abs
 import numpy as np
 import pytest
 
-from tests.test_gpu_parity import ATOL, RTOL, Scene, _as_u8, _bind_ctx, assert_close  # noqa: F401
+from tests.test_gpu_parity import (ATOL, RTOL, Scene, _as_u8, _bind_ctx,  # noqa: F401
+                                   assert_close, outlier_q)
 
 pytestmark = pytest.mark.gpu
 
@@ -28,7 +29,7 @@ def _oracle(rko, sc, seq, ctx, n, q, scale):
 
 
 def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, seed=0,
-         segment_tokens=None):
+         segment_tokens=None, q_outliers=False):
     """entries: (seq, ctx, n) with ctx + n <= the sequence's length.
     segment_tokens: None runs without a workspace (no split); otherwise the
     call gets the workspace rkv_prefill_workspace_bytes asks for."""
@@ -37,7 +38,8 @@ def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, 
     D = sc.D
     rows = [n for _, _, n in entries]
     total = max(sum(rows), 1)
-    q = rng.standard_normal((total, Hq, D)).astype(np.float32)
+    q = outlier_q(rng, (total, Hq, D)) if q_outliers else \
+        rng.standard_normal((total, Hq, D)).astype(np.float32)
     if q_bf16:
         q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
     qd = torch.from_numpy(q).cuda()
@@ -88,6 +90,22 @@ def test_prefill_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16, out_bf16
                src_bf16=q_bf16)
     ent = [(i, c, n) for i, (c, n) in enumerate(entries)]
     _run(rkv, rko, ctx, sc, ent, Hq, 1.0 / np.sqrt(D), q_bf16, out_bf16, seed=D + PT)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,PT,entries,q_bf16", [
+    (16, 2, 256, 64, [(0, 40), (300, 17), (129, 128), (1000, 70)], True),
+    (8, 2, 128, 16, [(0, 33), (200, 100), (31, 2)], False),
+    (32, 2, 128, 128, [(250, 23), (0, 9)], True),
+])
+def test_prefill_outlier_query(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16):
+    """Prefill rows whose queries carry x32 and x100 outlier channels, split
+    and unsplit, against the oracle's f32 q."""
+    lens = [c + n + 1 for c, n in entries]
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=7 + D + PT, outliers=0.01, src_bf16=True)
+    ent = [(i, c, n) for i, (c, n) in enumerate(entries)]
+    _run(rkv, rko, ctx, sc, ent, Hq, 1.0 / np.sqrt(D), q_bf16, seed=D, q_outliers=True)
+    _run(rkv, rko, ctx, sc, ent, Hq, 1.0 / np.sqrt(D), q_bf16, seed=D, q_outliers=True,
+         segment_tokens=128)
 
 
 @pytest.mark.parametrize("Hq,Hkv,D,PT,entries,seg,out_bf16", [
