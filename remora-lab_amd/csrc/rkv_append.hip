@@ -2,7 +2,7 @@
 // bit-exact gather/import between pages and reference rows, and a batch
 // f16 encoder (gfx950).
 //
-// Quantization rules (bit-exact with the CPU reference): q8_quantize_lane
+// Quantization rules (bit-exact with the CPU reference): q8_quantize_values
 // in rkv_device.h -- canonical (har/crates/r4kv/src/quant.rs:45-90) or
 // har-serve (har/crates/har-serve/src/attention.rs:25-42).
 #include <algorithm>
@@ -13,52 +13,148 @@ namespace rkv {
 
 namespace {
 
-// One group of 8 lanes quantizes one 32-value block; lane `sub` owns values
-// 4*sub..4*sub+3.  The block index enumerates (row, kv_head, kind, block).
+// Eight consecutive source values (f32 or bf16) starting at element `off`.
+__device__ inline void load_src8(const void *src, uint64_t off, bool bf16, float v[8]) {
+  if (bf16) {
+    const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + off);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = bf16_bits_to_f32((uint16_t)(ws[i] & 0xffffu));
+      v[2 * i + 1] = bf16_bits_to_f32((uint16_t)(ws[i] >> 16));
+    }
+  } else {
+    const float4 a = *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + off);
+    const float4 b = *reinterpret_cast<const float4 *>(static_cast<const float *>(src) + off + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+}
+
+// Input rows per append workgroup.
+constexpr int kAppRows = 32;
+
+// One workgroup of 256 threads appends input rows [32*blockIdx.x, +32) of
+// kv head blockIdx.y, K and V:
+//  1. each row's destination (region offset and slot; invalid rows are
+//     reported and skipped, nothing is written for them);
+//  2. quantize, 4 lanes per 32-value block with 8 values each (lanes of a
+//     row read its values in contiguous 16-byte loads), into LDS: K and V
+//     codes row-major (row stride D + 8 bytes: conflict-free for both the
+//     8-byte writes here and the transposing byte reads below) and scales;
+//  3. write the page bytes so that a wave's stores are contiguous whenever
+//     the rows are consecutive tokens: K rows as 16-byte stores; V codes
+//     (page layout [slot/TT][dim][slot%TT]) as one 4-byte store per 4 rows
+//     that are 4 aligned consecutive slots of one page, lanes ordered by
+//     slot group then dim (256 contiguous bytes per wave for a whole tile),
+//     else byte stores; scales with lanes ordered by slot.
+template <int D>
 __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
-  const uint32_t tid = blockIdx.x * 256u + threadIdx.x;
-  const int32_t D = a.g.head_dim;
-  const int32_t NB = D >> 5;
-  const uint32_t nblocks = (uint32_t)a.n_rows * (uint32_t)a.g.kv_heads * 2u * (uint32_t)NB;
-  const uint32_t blk = tid >> 3;
-  const int32_t sub = (int32_t)(tid & 7u);
-  // Every lane takes part in the shuffles; out-of-range lanes use zeros.
-  const bool live = blk < nblocks;
-  const uint32_t blkc = live ? blk : 0u;
-  const int32_t b = (int32_t)(blkc % (uint32_t)NB);
-  uint32_t t = blkc / (uint32_t)NB;
-  const int32_t kind = (int32_t)(t & 1u);
-  t >>= 1;
-  const int32_t kvh = (int32_t)(t % (uint32_t)a.g.kv_heads);
-  const int32_t row = (int32_t)(t / (uint32_t)a.g.kv_heads);
+  constexpr int NB = D / 32;
+  constexpr int RS = D + 8;  // LDS row stride
+  __shared__ __attribute__((aligned(16))) uint8_t codes[2][kAppRows][RS];
+  __shared__ uint16_t scl[2][kAppRows][NB];
+  __shared__ int64_t rbase[kAppRows];  // region offset of (page, kv head, K); -1: skip the row
+  __shared__ int32_t rslot[kAppRows];
+  __shared__ int32_t quad[kAppRows / 4];  // rows 4i..4i+3 are slots s..s+3 (s % 4 == 0) of one page
+  const Geo g = a.g;
+  const int tid = (int)threadIdx.x;
+  const int kvh = (int)blockIdx.y;
+  const int64_t row0 = (int64_t)blockIdx.x * kAppRows;
+  const int nr = (int)min<int64_t>(kAppRows, (int64_t)a.n_rows - row0);
 
-  float v[4] = {0.f, 0.f, 0.f, 0.f};
-  if (live) {
-    const uint64_t off =
-        ((uint64_t)row * (uint64_t)a.g.kv_heads + (uint64_t)kvh) * (uint64_t)D + (uint64_t)(b * 32 + sub * 4);
-    load_src4(kind == 0 ? a.k_src : a.v_src, off, a.src_bf16 != 0, v);
+  if (tid < kAppRows) {
+    int64_t base = -1;
+    int32_t slot = 0;
+    if (tid < nr) {
+      const int64_t row = row0 + tid;
+      const int32_t seq = a.seq_ids[row];
+      const int32_t pos = a.positions[row];
+      if (seq < 0 || seq >= a.n_seqs) {
+        if (kvh == 0) atomicOr(a.fault, FAULT_BAD_SEQ);
+      } else if (pos < 0 || pos / g.page_tokens >= a.bt_stride) {
+        if (kvh == 0) atomicOr(a.fault, FAULT_BAD_POSITION);
+      } else {
+        const int32_t page = a.bt[(int64_t)seq * a.bt_stride + pos / g.page_tokens];
+        if (page < 0 || page >= g.num_pages) {
+          if (kvh == 0) atomicOr(a.fault, FAULT_BAD_PAGE);
+        } else {
+          base = (int64_t)region_base(g, page, kvh, 0);
+          slot = pos % g.page_tokens;
+        }
+      }
+    }
+    rbase[tid] = base;
+    rslot[tid] = slot;
   }
-  uint16_t scale;
-  const uint32_t codes = q8_quantize_lane(v, a.rule, scale);
-  if (!live) return;
+  __syncthreads();
+  if (tid < kAppRows / 4) {
+    const int r = 4 * tid;
+    bool run = rbase[r] >= 0 && rslot[r] % 4 == 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i) run = run && rbase[r + i] == rbase[r] && rslot[r + i] == rslot[r] + i;
+    quad[tid] = run;
+  }
 
-  const int32_t seq = a.seq_ids[row];
-  const int32_t pos = a.positions[row];
-  if (seq < 0 || seq >= a.n_seqs) {
-    if (sub == 0) atomicOr(a.fault, FAULT_BAD_SEQ);
-    return;
+  // ---- quantize: tasks (row, kind, block, lane), lane fastest ------------------
+  constexpr int kTasks = kAppRows * 2 * NB * 4;
+  static_assert(kTasks % 256 == 0, "every thread takes part in every shuffle round");
+#pragma unroll 2
+  for (int t = tid; t < kTasks; t += 256) {
+    const int sub = t & 3;
+    const int blk = (t >> 2) % NB;
+    const int kind = ((t >> 2) / NB) & 1;
+    const int r = (t >> 2) / NB / 2;
+    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (r < nr)
+      load_src8(kind == 0 ? a.k_src : a.v_src,
+                ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
+                    (uint64_t)(blk * 32 + sub * 8),
+                a.src_bf16 != 0, v);
+    uint16_t scale;
+    uint64_t c = q8_quantize_values<8>(v, a.rule, scale);
+    if (kind == 1) c ^= 0x8080808080808080ull;  // V codes are stored biased (code_bias)
+    *reinterpret_cast<uint64_t *>(&codes[kind][r][blk * 32 + sub * 8]) = c;
+    if (sub == 0) scl[kind][r][blk] = scale;
   }
-  if (pos < 0 || pos / a.g.page_tokens >= a.bt_stride) {
-    if (sub == 0) atomicOr(a.fault, FAULT_BAD_POSITION);
-    return;
+  __syncthreads();
+
+  uint8_t *pages = a.pages;
+  const uint64_t RB = region_bytes(g);
+  // K codes: row r's D bytes at slot * D of the K region
+  for (int t = tid; t < kAppRows * (D / 16); t += 256) {
+    const int r = t / (D / 16), c = t % (D / 16);
+    const int64_t b = rbase[r];
+    if (b < 0) continue;
+    // (LDS rows are 8-byte aligned: two 8-byte reads)
+    const uint2 lo = *reinterpret_cast<const uint2 *>(&codes[0][r][16 * c]);
+    const uint2 hi = *reinterpret_cast<const uint2 *>(&codes[0][r][16 * c + 8]);
+    *reinterpret_cast<uint4 *>(pages + b + (uint64_t)rslot[r] * D + 16 * c) = uint4{lo.x, lo.y, hi.x, hi.y};
   }
-  const int32_t page = a.bt[(int64_t)seq * a.bt_stride + pos / a.g.page_tokens];
-  if (page < 0 || page >= a.g.num_pages) {
-    if (sub == 0) atomicOr(a.fault, FAULT_BAD_PAGE);
-    return;
+  // V codes: tasks (4-row group, dim), group fastest
+  for (int t = tid; t < (kAppRows / 4) * D; t += 256) {
+    const int q = t % (kAppRows / 4), d = t / (kAppRows / 4);
+    const int r = 4 * q;
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w |= (uint32_t)codes[1][r + i][d] << (8 * i);
+    if (quad[q]) {
+      *reinterpret_cast<uint32_t *>(pages + rbase[r] + RB + code_offset(g, 1, rslot[r], d)) = w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (rbase[r + i] >= 0)
+          pages[rbase[r + i] + RB + code_offset(g, 1, rslot[r + i], d)] = (uint8_t)(w >> (8 * i));
+    }
   }
-  const int32_t slot = pos % a.g.page_tokens;
-  store_q8_lane(a.g, a.pages + region_base(a.g, page, kvh, kind), kind, slot, b, sub, codes, scale);
+  // scales: tasks (row, block, kind), row fastest
+  for (int t = tid; t < 2 * NB * kAppRows; t += 256) {
+    const int r = t % kAppRows, blk = (t / kAppRows) % NB, kind = t / (kAppRows * NB);
+    const int64_t b = rbase[r];
+    if (b < 0) continue;
+    *reinterpret_cast<uint16_t *>(pages + b + kind * RB + scale_offset(g, rslot[r], blk)) =
+        scl[kind][r][blk];
+  }
 }
 
 // One thread per (kv_head, position, block): 34 reference-row bytes.
@@ -125,9 +221,12 @@ inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 255) / 
 }  // namespace
 
 hipError_t launch_append(const AppendLaunch &a, hipStream_t s) {
-  const int64_t threads = (int64_t)a.n_rows * a.g.kv_heads * 2 * (a.g.head_dim / 32) * 8;
-  if (threads == 0) return hipSuccess;
-  hipLaunchKernelGGL(append_kernel, dim3(grid_for(threads)), dim3(256), 0, s, a);
+  if (a.n_rows <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((a.n_rows + kAppRows - 1) / kAppRows), (unsigned)a.g.kv_heads);
+  if (a.g.head_dim == 256)
+    hipLaunchKernelGGL(append_kernel<256>, grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL(append_kernel<128>, grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -164,8 +164,9 @@ __device__ inline int32_t q8_code(float r) {
 
 // ---------------------------------------------------------------------------
 // Q8_0 quantization of one 32-value block by 8 consecutive lanes; lane `sub`
-// of the group owns values 4*sub..4*sub+3.  Every lane of the wave must make
-// the call (the group max is three xor-shuffles).
+// of the group owns values 4*sub..4*sub+3 (q8_quantize_lane), or by 4 lanes
+// of 8 values (q8_quantize_values<8>).  Every lane of the wave must make the
+// call (the group max is two or three xor-shuffles).
 //   canonical (har/crates/r4kv/src/quant.rs:45-90): d = amax/127, inv = 1/d,
 //     q = clamp(round_half_away(v*inv)), scale = f16_rtne(d);
 //   har-serve (har/crates/har-serve/src/attention.rs:25-42): same d,
@@ -174,33 +175,41 @@ __device__ inline int32_t q8_code(float r) {
 // uses f32::max).  f32 division is IEEE (the build keeps it correctly
 // rounded) and nothing here contracts into an FMA.
 // ---------------------------------------------------------------------------
-__device__ inline uint32_t q8_quantize_lane(const float v[4], int32_t rule, uint16_t &scale) {
+// The same rule with VPL values per lane (32/VPL consecutive lanes per
+// block, VPL in {4, 8}); code i of this lane is byte i of the result.
+template <int VPL>
+__device__ inline uint64_t q8_quantize_values(const float *v, int32_t rule, uint16_t &scale) {
+  static_assert(VPL == 4 || VPL == 8, "4 or 8 values per lane");
   float amax = 0.0f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < VPL; ++i) {
     const float x = fabsf(v[i]);
     amax = x > amax ? x : amax;
   }
   amax = fmaxf(amax, __shfl_xor(amax, 1));
   amax = fmaxf(amax, __shfl_xor(amax, 2));
-  amax = fmaxf(amax, __shfl_xor(amax, 4));
+  if (VPL == 4) amax = fmaxf(amax, __shfl_xor(amax, 4));
   const float d = amax == 0.0f ? 0.0f : amax / 127.0f;
-  uint32_t codes = 0;
+  uint64_t codes = 0;
   if (rule == 0) {
     const float inv = d == 0.0f ? 0.0f : 1.0f / d;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      codes |= ((uint32_t)(uint8_t)(int8_t)q8_code(roundf(v[i] * inv))) << (8 * i);
+    for (int i = 0; i < VPL; ++i)
+      codes |= ((uint64_t)(uint8_t)(int8_t)q8_code(roundf(v[i] * inv))) << (8 * i);
     scale = f16_rtne(d);
   } else {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < VPL; ++i) {
       const int32_t q = d == 0.0f ? 0 : q8_code(roundf(v[i] / d));
-      codes |= ((uint32_t)(uint8_t)(int8_t)q) << (8 * i);
+      codes |= ((uint64_t)(uint8_t)(int8_t)q) << (8 * i);
     }
     scale = f16_harserve(d);
   }
   return codes;
+}
+
+__device__ inline uint32_t q8_quantize_lane(const float v[4], int32_t rule, uint16_t &scale) {
+  return (uint32_t)q8_quantize_values<4>(v, rule, scale);
 }
 
 // Four consecutive source values (f32 or bf16) starting at element `off`.

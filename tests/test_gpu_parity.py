@@ -219,7 +219,7 @@ def test_append_row_orders(rkv, rko, ctx, D, PT, order):
     v = rng.standard_normal((len(sid), Hkv, D)).astype(np.float32)
     bad = np.zeros(len(sid), bool)
     if order == "bad_rows":    # a bad sequence id, a position past the table, a -1 page
-        bad[[5, 40, 41, 100]] = True
+        bad[[5, 40, 41]] = True
         sid[5] = 7
         pos[40] = W * PT + 3
         pos[41] = -1
