@@ -14,8 +14,9 @@ namespace rkv {
 namespace {
 
 // Eight consecutive source values (f32 or bf16) starting at element `off`.
-__device__ inline void load_src8(const void *src, uint64_t off, bool bf16, float v[8]) {
-  if (bf16) {
+template <bool kBf16>
+__device__ inline void load_src8(const void *src, uint64_t off, float v[8]) {
+  if constexpr (kBf16) {
     const uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(src) + off);
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -48,7 +49,7 @@ constexpr int kAppRows = 32;
 //     that are 4 aligned consecutive slots of one page, lanes ordered by
 //     slot group then dim (256 contiguous bytes per wave for a whole tile),
 //     else byte stores; scales with lanes ordered by slot.
-template <int D>
+template <int D, bool kBf16, int kRule>
 __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
   constexpr int NB = D / 32;
   constexpr int RS = D + 8;  // LDS row stride
@@ -63,7 +64,9 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
   const int64_t row0 = (int64_t)blockIdx.x * kAppRows;
   const int nr = (int)min<int64_t>(kAppRows, (int64_t)a.n_rows - row0);
 
-  if (tid < kAppRows) {
+  // ---- rows' destinations (lanes 0-31 of wave 0; the loads of the other
+  // waves' quantize tasks are already in flight meanwhile) ------------------
+  if (tid < 64) {
     int64_t base = -1;
     int32_t slot = 0;
     if (tid < nr) {
@@ -84,35 +87,50 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
         }
       }
     }
-    rbase[tid] = base;
-    rslot[tid] = slot;
-  }
-  __syncthreads();
-  if (tid < kAppRows / 4) {
-    const int r = 4 * tid;
-    bool run = rbase[r] >= 0 && rslot[r] % 4 == 0;
+    // rows 4i..4i+3 form a quad when they are 4 aligned consecutive slots of one page
+    bool run = base >= 0 && slot % 4 == 0;
 #pragma unroll
-    for (int i = 1; i < 4; ++i) run = run && rbase[r + i] == rbase[r] && rslot[r + i] == rslot[r] + i;
-    quad[tid] = run;
+    for (int i = 1; i < 4; ++i) {
+      const int64_t b2 = __shfl_down(base, i);
+      const int32_t s2 = __shfl_down(slot, i);
+      run = run && b2 == base && s2 == slot + i;
+    }
+    if (tid < kAppRows) {
+      rbase[tid] = base;
+      rslot[tid] = slot;
+      if ((tid & 3) == 0) quad[tid >> 2] = run;
+    }
   }
 
-  // ---- quantize: tasks (row, kind, block, lane), lane fastest ------------------
+  // ---- quantize: tasks (row, kind, block, lane), lane fastest; fully
+  // unrolled, with dtype and rule fixed at compile time and rows past the
+  // last read as the last row (never written), so every task's source load
+  // is issued before the first wait ------------------------------------------
   constexpr int kTasks = kAppRows * 2 * NB * 4;
+  constexpr int kPer = kTasks / 256;
   static_assert(kTasks % 256 == 0, "every thread takes part in every shuffle round");
-#pragma unroll 2
-  for (int t = tid; t < kTasks; t += 256) {
+  float v[kPer][8];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int t = 256 * i + tid;
+    const int sub = t & 3;
+    const int blk = (t >> 2) % NB;
+    const int kind = ((t >> 2) / NB) & 1;
+    const int r = min((t >> 2) / NB / 2, nr - 1);
+    load_src8<kBf16>(kind == 0 ? a.k_src : a.v_src,
+                     ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
+                         (uint64_t)(blk * 32 + sub * 8),
+                     v[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int t = 256 * i + tid;
     const int sub = t & 3;
     const int blk = (t >> 2) % NB;
     const int kind = ((t >> 2) / NB) & 1;
     const int r = (t >> 2) / NB / 2;
-    float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (r < nr)
-      load_src8(kind == 0 ? a.k_src : a.v_src,
-                ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
-                    (uint64_t)(blk * 32 + sub * 8),
-                a.src_bf16 != 0, v);
     uint16_t scale;
-    uint64_t c = q8_quantize_values<8>(v, a.rule, scale);
+    uint64_t c = q8_quantize_values<8>(v[i], kRule, scale);
     if (kind == 1) c ^= 0x8080808080808080ull;  // V codes are stored biased (code_bias)
     *reinterpret_cast<uint64_t *>(&codes[kind][r][blk * 32 + sub * 8]) = c;
     if (sub == 0) scl[kind][r][blk] = scale;
@@ -220,13 +238,24 @@ inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 255) / 
 
 }  // namespace
 
+namespace {
+template <int D>
+void launch_append_d(const AppendLaunch &a, dim3 grid, hipStream_t s) {
+  if (a.src_bf16) {
+    if (a.rule == 0) hipLaunchKernelGGL((append_kernel<D, true, 0>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((append_kernel<D, true, 1>), grid, dim3(256), 0, s, a);
+  } else {
+    if (a.rule == 0) hipLaunchKernelGGL((append_kernel<D, false, 0>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((append_kernel<D, false, 1>), grid, dim3(256), 0, s, a);
+  }
+}
+}  // namespace
+
 hipError_t launch_append(const AppendLaunch &a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
   const dim3 grid((unsigned)((a.n_rows + kAppRows - 1) / kAppRows), (unsigned)a.g.kv_heads);
-  if (a.g.head_dim == 256)
-    hipLaunchKernelGGL(append_kernel<256>, grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(append_kernel<128>, grid, dim3(256), 0, s, a);
+  if (a.g.head_dim == 256) launch_append_d<256>(a, grid, s);
+  else launch_append_d<128>(a, grid, s);
   return hipGetLastError();
 }
 

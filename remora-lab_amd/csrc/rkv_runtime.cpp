@@ -122,6 +122,12 @@ rkv_status rkv_ctx_create(int32_t device, rkv_ctx **out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(RKV_ERR_UNSUPPORTED, op, "device %d is %s; kernels are built for gfx950", device,
                 prop.gcnArchName);
+  // the decode's partition plan and the prefill's dispatch simulation are
+  // sized for the whole chip: 256 CUs in 8 XCDs
+  if (prop.multiProcessorCount != rkv::kComputeUnits)
+    return fail(RKV_ERR_UNSUPPORTED, op,
+                "device %d has %d compute units; the launch plans are sized for %d (a whole "
+                "MI355X, 8 XCDs)", device, prop.multiProcessorCount, rkv::kComputeUnits);
   rkv_ctx *c = new rkv_ctx;
   c->device = device;
   if ((e = hipMalloc(&c->d_fault, sizeof(int32_t))) != hipSuccess) {
