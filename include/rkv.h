@@ -249,6 +249,23 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
                          const int32_t *block_tables, int32_t bt_stride,
                          const int32_t *seq_lens, int32_t n_seqs,
                          const rkv_decode_args *args, void *stream);
+/* rkv_decode_q8 that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  args->workspace and workspace_bytes are
+ * ignored: the split-K partials go to a static device array of
+ * RKV_DECODE_SCRATCH_BYTES that the library holds on each device it runs on
+ * until the process ends.  A launch whose partials need more (see
+ * rkv_decode_workspace_bytes) is refused with RKV_ERR_INVALID_ARG.  Every
+ * call on one device shares that array, and a call leaves its contents
+ * behind (no call needs them cleared): calls that overlap on one device --
+ * queued on different streams, or from several threads -- race and give
+ * wrong results; calls queued on one stream are ordered. */
+#define RKV_DECODE_SCRATCH_BYTES ((size_t)64 << 20)
+rkv_status rkv_decode_q8_noalloc(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                                 const int32_t *block_tables, int32_t bt_stride,
+                                 const int32_t *seq_lens, int32_t n_seqs,
+                                 const rkv_decode_args *args, void *stream);
 /* Workspace bytes rkv_decode_q8 needs for these arguments (0 if none); it
  * depends on batch, q_len, q_heads, max_seq_len and partition_tokens, and
  * needs no initialisation. */

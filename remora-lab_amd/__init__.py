@@ -158,6 +158,8 @@ _SIGS = {
                                   C.POINTER(AppendArgs), P]),
     "rkv_decode_q8": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P, C.c_int32,
                                   C.POINTER(DecodeArgs), P]),
+    "rkv_decode_q8_noalloc": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P, C.c_int32,
+                                          C.POINTER(DecodeArgs), P]),
     "rkv_decode_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
     "rkv_prefill_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(PrefillArgs)]),
     "rkv_decode_partition_tokens": (C.c_int32, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
@@ -541,6 +543,18 @@ def decode_q8(ctx: Ctx, g: Geometry, pages, block_tables, seq_lens, a: DecodeArg
     check(lib().rkv_decode_q8(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables),
                               block_tables.shape[-1], _ptr(seq_lens), seq_lens.numel(),
                               C.byref(a), _stream(stream)))
+
+
+DECODE_SCRATCH_BYTES = 64 << 20  # RKV_DECODE_SCRATCH_BYTES
+
+
+def decode_q8_noalloc(ctx: Ctx, g: Geometry, pages, block_tables, seq_lens, a: DecodeArgs,
+                      stream=None) -> None:
+    """rkv_decode_q8 with the partials in the library's static device
+    scratch: a.workspace is ignored and nothing is allocated."""
+    check(lib().rkv_decode_q8_noalloc(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables),
+                                      block_tables.shape[-1], _ptr(seq_lens), seq_lens.numel(),
+                                      C.byref(a), _stream(stream)))
 
 
 def decode_q8_partials(ctx: Ctx, g: Geometry, pages, block_tables, seq_lens, a: DecodeArgs,

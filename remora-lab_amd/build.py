@@ -16,7 +16,7 @@ OUT = os.path.join(HERE, "librkv.so")
 OBJDIR = os.path.join(HERE, "_build")
 
 SOURCES = ["rkv_append.hip", "rkv_decode.hip", "rkv_decode_rows32.hip", "rkv_prefill.hip",
-           "rkv_r4kv.hip", "rkv_stream.hip", "rkv_runtime.cpp", "rkv_serve.cpp"]
+           "rkv_r4kv.hip", "rkv_stream.hip", "rkv_scratch.hip", "rkv_runtime.cpp", "rkv_serve.cpp"]
 
 # Per-file extra flags.  rkv_decode.hip: MFMA destinations and accumulators
 # in VGPRs (no AGPR<->VGPR copies around the VALU work on them).  The

@@ -177,7 +177,13 @@ constexpr int decode_wgs_per_cu(int head_dim, int rows, int stages) {
   const int by_regs = (head_dim == 256 || rows > 16) ? 4 : 8;
   return by_lds < by_regs ? by_lds : by_regs;
 }
-constexpr int kComputeUnits = 256;  // MI355X (gfx950)
+constexpr int kComputeUnits = 256;  // MI355X (gfx950): 8 XCDs of 32 CUs
+
+// Static device scratch of rkv_decode_q8_noalloc (rkv_scratch.hip): its
+// size, and its device address on `device`, which must be the current
+// device (resolved once per device, then cached).
+constexpr size_t kDecodeScratchBytes = 64u << 20;
+hipError_t scratch_address(int device, void **ptr);
 
 struct CombineLaunch {
   const float *ml;

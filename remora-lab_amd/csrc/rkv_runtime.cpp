@@ -89,6 +89,7 @@ hipStream_t as_stream(void *s) { return static_cast<hipStream_t>(s); }
 struct rkv_ctx {
   int32_t device = 0;
   int32_t *d_fault = nullptr;  // device fault word (rkv::FAULT_* bits)
+  void *scratch = nullptr;     // this device's static decode scratch (rkv_scratch.hip)
 };
 
 namespace rkv {
@@ -128,8 +129,13 @@ rkv_status rkv_ctx_create(int32_t device, rkv_ctx **out) {
     return fail(RKV_ERR_UNSUPPORTED, op,
                 "device %d has %d compute units; the launch plans are sized for %d (a whole "
                 "MI355X, 8 XCDs)", device, prop.multiProcessorCount, rkv::kComputeUnits);
+  // the static decode scratch of rkv_decode_q8_noalloc, resolved once per
+  // device with the device current
+  void *scratch = nullptr;
+  if ((e = rkv::scratch_address(device, &scratch)) != hipSuccess) return hip_fail(op, e);
   rkv_ctx *c = new rkv_ctx;
   c->device = device;
+  c->scratch = scratch;
   if ((e = hipMalloc(&c->d_fault, sizeof(int32_t))) != hipSuccess) {
     delete c;
     return hip_fail(op, e);
@@ -1050,6 +1056,27 @@ rkv_status rkv_decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pag
                          const int32_t *seq_lens, int32_t n_seqs, const rkv_decode_args *a,
                          void *stream) {
   return decode_q8(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, a, stream,
+                   decode_stages());
+}
+
+rkv_status rkv_decode_q8_noalloc(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                                 const int32_t *block_tables, int32_t bt_stride,
+                                 const int32_t *seq_lens, int32_t n_seqs,
+                                 const rkv_decode_args *a, void *stream) {
+  const char *op = "rkv_decode_q8_noalloc";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_decode(g, a, op)) return s;
+  if (!ctx->scratch) return fail(RKV_ERR_DEVICE, op, "no static scratch on device %d", ctx->device);
+  const size_t need = ws_bytes(g, a, plan_of(g, a, decode_stages()));
+  if (need > rkv::kDecodeScratchBytes)
+    return fail(RKV_ERR_INVALID_ARG, op,
+                "the split-K partials need %zu bytes, more than the %zu-byte static scratch "
+                "(fewer entries, shorter max_seq_len or longer partitions fit; rkv_decode_q8 "
+                "takes a workspace of any size)", need, rkv::kDecodeScratchBytes);
+  rkv_decode_args b = *a;
+  b.workspace = ctx->scratch;
+  b.workspace_bytes = rkv::kDecodeScratchBytes;
+  return decode_q8(ctx, g, pages, block_tables, bt_stride, seq_lens, n_seqs, &b, stream,
                    decode_stages());
 }
 
