@@ -364,18 +364,23 @@ def cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv, D, scal
     qs = (qf[:n_all, 0] * np.float32(scale)).astype(np.float32)
     max_err = 0.0
     t0 = time.perf_counter()
+    refs = []
     for s in range(n_sample):
         ref = rko.flash_decode_reference(p, rows[s][0], rows[s][1], qs[s].reshape(-1))
-        max_err = max(max_err, float(np.max(np.abs(ref - gpu_out[s, 0].reshape(-1)))))
+        refs.append(ref)
     t_dec = time.perf_counter() - t0
+    for s, ref in enumerate(refs):
+        max_err = max(max_err, float(np.max(np.abs(ref - gpu_out[s, 0].reshape(-1)))))
     full = t_app + t_dec * B / n_sample
     threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
     t0 = time.perf_counter()
     many = rko.flash_decode_reference_many(p, [r[0] for r in rows], [r[1] for r in rows], qs, threads)
     t_many = time.perf_counter() - t0
     max_err = max(max_err, float(np.max(np.abs(many - gpu_out[:n_all, 0]))))
+    rel_err = float(np.linalg.norm(many - gpu_out[:n_all, 0]) / np.linalg.norm(many))
     full_all = t_app + t_many * B / n_all
     return {"value": round(step_bytes / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": f"append quantize of all {B} rows + flash_decode_reference (attention.rs:148-215, "
                       f"chunk 1024) over {n_sample} of {B} sequences at L={L}, scaled x{B / n_sample:g}; "
                       f"{t_app + t_dec:.1f} s of CPU work",
@@ -385,7 +390,20 @@ def cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv, D, scal
                           "sample": f"the same loop over {n_all} of {B} sequences on {threads} OpenMP "
                                     f"threads (sequence x q head), scaled x{B / n_all:g}; "
                                     f"{t_many:.1f} s wall"},
-            "gpu_vs_cpu_max_abs_err_on_sample": max_err}
+            "gpu_vs_cpu_max_abs_err_on_sample": max_err,
+            "gpu_vs_cpu_rel_err_on_sample": rel_err}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as "Model name")."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 # ---------------------------------------------------------------------------
