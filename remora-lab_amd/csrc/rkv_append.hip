@@ -32,11 +32,10 @@ __device__ inline void load_src8(const void *src, uint64_t off, float v[8]) {
   }
 }
 
-// Input rows per append workgroup.
-constexpr int kAppRows = 32;
-
-// One workgroup of 256 threads appends input rows [32*blockIdx.x, +32) of
-// kv head blockIdx.y, K and V:
+// One workgroup of 256 threads appends input rows [ROWS*blockIdx.x, +ROWS)
+// of kv head blockIdx.y, K and V (ROWS = 32 for large launches, 8 for small
+// ones, so that a few thousand rows still spread over several workgroups per
+// CU: the quantizer's VALU work, not HBM, bounds a workgroup):
 //  1. each row's destination (region offset and slot; invalid rows are
 //     reported and skipped, nothing is written for them);
 //  2. quantize, 4 lanes per 32-value block with 8 values each (lanes of a
@@ -49,8 +48,9 @@ constexpr int kAppRows = 32;
 //     that are 4 aligned consecutive slots of one page, lanes ordered by
 //     slot group then dim (256 contiguous bytes per wave for a whole tile),
 //     else byte stores; scales with lanes ordered by slot.
-template <int D, bool kBf16, int kRule>
+template <int D, int kAppRows, bool kBf16, int kRule>
 __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
+  static_assert(kAppRows % 4 == 0 && kAppRows <= 64, "rows come in quads, resolved by wave 0");
   constexpr int NB = D / 32;
   constexpr int RS = D + 8;  // LDS row stride
   __shared__ __attribute__((aligned(16))) uint8_t codes[2][kAppRows][RS];
@@ -239,23 +239,31 @@ inline unsigned grid_for(int64_t threads) { return (unsigned)((threads + 255) / 
 }  // namespace
 
 namespace {
-template <int D>
-void launch_append_d(const AppendLaunch &a, dim3 grid, hipStream_t s) {
+template <int D, int ROWS>
+void launch_append_r(const AppendLaunch &a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.n_rows + ROWS - 1) / ROWS), (unsigned)a.g.kv_heads);
   if (a.src_bf16) {
-    if (a.rule == 0) hipLaunchKernelGGL((append_kernel<D, true, 0>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((append_kernel<D, true, 1>), grid, dim3(256), 0, s, a);
+    if (a.rule == 0) hipLaunchKernelGGL((append_kernel<D, ROWS, true, 0>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((append_kernel<D, ROWS, true, 1>), grid, dim3(256), 0, s, a);
   } else {
-    if (a.rule == 0) hipLaunchKernelGGL((append_kernel<D, false, 0>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((append_kernel<D, false, 1>), grid, dim3(256), 0, s, a);
+    if (a.rule == 0) hipLaunchKernelGGL((append_kernel<D, ROWS, false, 0>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((append_kernel<D, ROWS, false, 1>), grid, dim3(256), 0, s, a);
   }
+}
+template <int D>
+void launch_append_d(const AppendLaunch &a, hipStream_t s) {
+  // 32-row workgroups once there are at least 8 per CU, else 8-row ones
+  if ((int64_t)a.n_rows * a.g.kv_heads >= (int64_t)32 * 8 * kComputeUnits)
+    launch_append_r<D, 32>(a, s);
+  else
+    launch_append_r<D, 8>(a, s);
 }
 }  // namespace
 
 hipError_t launch_append(const AppendLaunch &a, hipStream_t s) {
   if (a.n_rows <= 0) return hipSuccess;
-  const dim3 grid((unsigned)((a.n_rows + kAppRows - 1) / kAppRows), (unsigned)a.g.kv_heads);
-  if (a.g.head_dim == 256) launch_append_d<256>(a, grid, s);
-  else launch_append_d<128>(a, grid, s);
+  if (a.g.head_dim == 256) launch_append_d<256>(a, s);
+  else launch_append_d<128>(a, s);
   return hipGetLastError();
 }
 

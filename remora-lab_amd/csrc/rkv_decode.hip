@@ -55,32 +55,26 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineLaunch c) {
   else static_cast<float *>(c.out)[oi] = r;
 }
 
-// Flat-layout combine.  Block (row, entry, split) merges partitions
-// [chunk*split, chunk*(split+1)) of the entry (from the header the decode
-// wrote).  Up to 16 partitions: one thread per dimension,
-// all loads in one round, no LDS.  More: groups of head_dim/4 threads (4 dims
-// each, float4 loads), group g taking partitions g, g + groups, ... 16 at a
-// time, merged online (running max, rescaled sums), then the groups merge
-// through LDS.  With one split per row the block writes the output; with
-// more it stores its (m, l, o) and combine_splits_kernel merges the splits in
-// a second launch.  All merges are the chunk combine of attention.rs:205-212
-// in base 2.
-struct Merge {
-  float m, l;
-  float4 o;
-  __device__ void add(float mi, float li, float4 oi) {
-    if (mi == -INFINITY) return;
-    const float mn = fmaxf(m, mi);
-    const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
-    const float w = __builtin_amdgcn_exp2f(mi - mn);
-    l = l * a + li * w;
-    o.x = o.x * a + oi.x * w;
-    o.y = o.y * a + oi.y * w;
-    o.z = o.z * a + oi.z * w;
-    o.w = o.w * a + oi.w * w;
-    m = mn;
-  }
-};
+// Flat-layout combine.  Block (row, entry, slice) merges all of the entry's
+// partitions (from the header the decode wrote) for one slice of the row's
+// dimensions.  With one slice and up to 16 partitions: one thread per
+// dimension, all loads in one round, no LDS.  Otherwise the slice's
+// head_dim/slices dims are read as float4s by LP lanes per partition and the
+// block's 256/LP lane groups take partitions g, g + groups, ...  Every block
+// first merges the row's (m, l) pairs into (M, L) and then sums
+// o_i * 2^(m_i - M) over its partitions; the o loads of the first 8
+// partitions per group are issued before the (m, l) loads, so both land in
+// one round.  Slicing by dimension gives rows with long partition lists
+// (config 3: 16 rows, 512 partitions) enough blocks in one launch, with no
+// second launch to merge splits.  All merges are the chunk combine of
+// attention.rs:205-212 in base 2.
+__device__ __forceinline__ void merge_ml(float &m, float &l, float m2, float l2) {
+  const float mn = fmaxf(m, m2);
+  const float a = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - mn);
+  const float b = m2 == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m2 - mn);
+  l = l * a + l2 * b;
+  m = mn;
+}
 
 __device__ __forceinline__ void store_res(const FlatCombineLaunch &c, int64_t oi, float4 res) {
   if (c.out_bf16) {
@@ -93,20 +87,9 @@ __device__ __forceinline__ void store_res(const FlatCombineLaunch &c, int64_t oi
   }
 }
 
-__device__ __forceinline__ void store_row(const FlatCombineLaunch &c, int64_t orow, int dt,
-                                          const Merge &t) {
-  const float inv = t.l > 0.0f ? 1.0f / t.l : 0.0f;
-  const float4 res = t.l > 0.0f ? float4{t.o.x * inv, t.o.y * inv, t.o.z * inv, t.o.w * inv}
-                                : float4{0.f, 0.f, 0.f, 0.f};
-  store_res(c, orow * c.head_dim + 4 * dt, res);
-}
-
-constexpr int kCombineThreads = 256;
-
-__global__ __launch_bounds__(kCombineThreads) void combine_flat_kernel(FlatCombineLaunch c) {
+__global__ __launch_bounds__(256) void combine_flat_kernel(FlatCombineLaunch c) {
   const int row = blockIdx.x;  // j * q_heads + h
   const int b = blockIdx.y;
-  const int split = blockIdx.z;
   const int t = threadIdx.x;
   const int j = row / c.q_heads, h = row % c.q_heads;
   const int q_per_kv = c.q_heads / c.kv_heads;
@@ -116,14 +99,10 @@ __global__ __launch_bounds__(kCombineThreads) void combine_flat_kernel(FlatCombi
   const int32_t start = c.hdr[1 + 2 * b];
   int32_t n = c.hdr[2 + 2 * b];
   if (start < 0 || n < 1 || start > c.n_wg - n) n = 0;
-  const int32_t n_splits = n > 0 ? (n + c.chunk - 1) / c.chunk : 1;
-  if (split >= n_splits) return;
-  const int32_t i_beg = split * c.chunk;
-  const int32_t i_end = min(n, i_beg + c.chunk);
   const int64_t p0 = ((int64_t)kvh * c.n_wg + start) * R + r;  // partition i at p0 + i*R
   const int64_t orow = (int64_t)b * c.q_len * c.q_heads + row;
 
-  if (c.splits == 1 && n <= 16) {
+  if (gridDim.z == 1 && n <= 16) {
     // one thread per dimension
     if (t >= c.head_dim) return;
     float2 ml[16];
@@ -154,73 +133,91 @@ __global__ __launch_bounds__(kCombineThreads) void combine_flat_kernel(FlatCombi
     return;
   }
 
-  const int GS = c.head_dim / 4;          // threads per group
-  const int NG = kCombineThreads / GS;    // groups
-  const int grp = t / GS, dt = t % GS;
-  Merge mg{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
-  for (int32_t i0 = i_beg + grp; i0 < i_end; i0 += 16 * NG) {
-    float2 ml[16];
-    float4 ov[16];
+  const int CH = c.head_dim / (int)gridDim.z;  // dims of this slice (>= 16)
+  const int LP = CH / 4;                       // lanes per partition
+  const int NG = 256 / LP;                     // partition groups
+  const int grp = t / LP, dt = t % LP;
+  const int dim = blockIdx.z * CH + 4 * dt;
+  const int lane = t & 63, wave = t >> 6;
+
+  constexpr int kB = 8;  // partitions per group and load round
+  // first batch of this group's partitions: o and m
+  float mi[kB];
+  float4 ov[kB];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+  for (int k = 0; k < kB; ++k) {
+    const int32_t i = grp + k * NG;
+    const int64_t pr = p0 + (int64_t)i * R;
+    const bool in = i < n;
+    ov[k] = in ? *reinterpret_cast<const float4 *>(c.o + pr * c.head_dim + dim)
+               : float4{0.f, 0.f, 0.f, 0.f};
+    mi[k] = in ? c.ml[2 * pr] : -INFINITY;
+  }
+
+  // (M, L) of the row over all n partitions
+  float m = -INFINITY, l = 0.0f;
+  for (int32_t i = t; i < n; i += 256) {
+    const float2 v = *reinterpret_cast<const float2 *>(c.ml + 2 * (p0 + (int64_t)i * R));
+    merge_ml(m, l, v.x, v.y);
+  }
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
+    merge_ml(m, l, m2, l2);
+  }
+  __shared__ float s_m[4], s_l[4];
+  __shared__ float4 s_o[4][64];
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
+  __syncthreads();
+  float M = s_m[0], L = s_l[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) merge_ml(M, L, s_m[w], s_l[w]);
+
+  float4 acc{0.f, 0.f, 0.f, 0.f};
+  for (int32_t i0 = grp;;) {
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
+      const float w = mi[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mi[k] - M);
+      acc.x += ov[k].x * w;
+      acc.y += ov[k].y * w;
+      acc.z += ov[k].z * w;
+      acc.w += ov[k].w * w;
+    }
+    i0 += kB * NG;
+    if (i0 >= n) break;
+#pragma unroll
+    for (int k = 0; k < kB; ++k) {
       const int32_t i = i0 + k * NG;
       const int64_t pr = p0 + (int64_t)i * R;
-      const bool in = i < i_end;
-      ml[k] = in ? *reinterpret_cast<const float2 *>(c.ml + 2 * pr) : float2{-INFINITY, 0.0f};
-      ov[k] = in ? *reinterpret_cast<const float4 *>(c.o + pr * c.head_dim + 4 * dt)
+      const bool in = i < n;
+      ov[k] = in ? *reinterpret_cast<const float4 *>(c.o + pr * c.head_dim + dim)
                  : float4{0.f, 0.f, 0.f, 0.f};
+      mi[k] = in ? c.ml[2 * pr] : -INFINITY;
     }
-#pragma unroll
-    for (int k = 0; k < 16; ++k) mg.add(ml[k].x, ml[k].y, ov[k]);
   }
-
-  __shared__ float s_m[8], s_l[8];
-  __shared__ float4 s_o[8][64];
-  if (dt == 0) {
-    s_m[grp] = mg.m;
-    s_l[grp] = mg.l;
+  // sum over the groups: lanes LP apart in a wave, then the 4 waves
+  for (int off = LP; off < 64; off <<= 1) {
+    acc.x += __shfl_xor(acc.x, off);
+    acc.y += __shfl_xor(acc.y, off);
+    acc.z += __shfl_xor(acc.z, off);
+    acc.w += __shfl_xor(acc.w, off);
   }
-  s_o[grp][dt] = mg.o;
+  if (lane < LP) s_o[wave][lane] = acc;
   __syncthreads();
-  if (grp != 0) return;
-  Merge tot{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
-  for (int g = 0; g < NG; ++g) tot.add(s_m[g], s_l[g], s_o[g][dt]);
-  if (c.splits == 1) {
-    store_row(c, orow, dt, tot);
-    return;
-  }
-  if (dt == 0)
-    *reinterpret_cast<float2 *>(c.split_ml + 2 * (orow * c.splits + split)) = float2{tot.m, tot.l};
-  *reinterpret_cast<float4 *>(c.split_o + (orow * c.splits + split) * c.head_dim + 4 * dt) = tot.o;
-}
-
-// Second level: merge the splits of every (row, entry), head_dim/4 threads.
-__global__ __launch_bounds__(64) void combine_splits_kernel(FlatCombineLaunch c) {
-  const int row = blockIdx.x;
-  const int b = blockIdx.y;
-  const int dt = threadIdx.x;
-  if (dt >= c.head_dim / 4) return;
-  int32_t n = c.hdr[2 + 2 * b];
-  const int32_t start = c.hdr[1 + 2 * b];
-  if (start < 0 || n < 1 || start > c.n_wg - n) n = 0;
-  const int32_t n_splits = n > 0 ? min(c.splits, (n + c.chunk - 1) / c.chunk) : 0;
-  const int64_t orow = (int64_t)b * c.q_len * c.q_heads + row;
-  Merge tot{-INFINITY, 0.0f, {0.f, 0.f, 0.f, 0.f}};
-  for (int32_t q0 = 0; q0 < n_splits; q0 += 8) {
-    float2 ml[8];
-    float4 ov[8];
+  if (t >= LP) return;
+  float4 o = s_o[0][t];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const bool in = q0 + k < n_splits;
-      const int64_t sp = orow * c.splits + q0 + k;
-      ml[k] = in ? *reinterpret_cast<const float2 *>(c.split_ml + 2 * sp) : float2{-INFINITY, 0.0f};
-      ov[k] = in ? *reinterpret_cast<const float4 *>(c.split_o + sp * c.head_dim + 4 * dt)
-                 : float4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k) tot.add(ml[k].x, ml[k].y, ov[k]);
+  for (int w = 1; w < 4; ++w) {
+    o.x += s_o[w][t].x;
+    o.y += s_o[w][t].y;
+    o.z += s_o[w][t].z;
+    o.w += s_o[w][t].w;
   }
-  store_row(c, orow, dt, tot);
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  store_res(c, orow * c.head_dim + dim, float4{o.x * inv, o.y * inv, o.z * inv, o.w * inv});
 }
 
 template <int D, int NS>
@@ -244,10 +241,11 @@ hipError_t launch_decode(const DecodeLaunch &d, hipStream_t s) {
 
 hipError_t launch_combine_flat(const FlatCombineLaunch &c, hipStream_t s) {
   if (c.batch == 0) return hipSuccess;
-  const dim3 grid((unsigned)(c.q_len * c.q_heads), (unsigned)c.batch);
-  hipLaunchKernelGGL(combine_flat_kernel, dim3(grid.x, grid.y, (unsigned)c.splits),
-                     dim3(kCombineThreads), 0, s, c);
-  if (c.splits > 1) hipLaunchKernelGGL(combine_splits_kernel, grid, dim3(64), 0, s, c);
+  if (c.slices < 1 || (c.slices & (c.slices - 1)) || c.head_dim % c.slices || c.head_dim / c.slices < 16 ||
+      c.head_dim / c.slices > 256)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(c.q_len * c.q_heads), (unsigned)c.batch, (unsigned)c.slices);
+  hipLaunchKernelGGL(combine_flat_kernel, grid, dim3(256), 0, s, c);
   return hipGetLastError();
 }
 

@@ -1085,23 +1085,26 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   dc.tok_end = tok_end;
   dc.n_tiles = tok_end > tok0 ? (tok_end - tok0 + kTile - 1) / kTile : 0;
 
-  // ---- rows appended by this launch: checked once per batch entry; written
-  // by the partition that holds their position, before its copies read them
-  dc.app_mode = 0;
-  if (p.app_k != nullptr) {
-    if (part == 0 && kvh == 0 && threadIdx.x < p.q_len) {
-      const int32_t row = b * p.q_len + lane;
-      const int32_t pos = p.app_pos[row];
-      if (p.app_seq_ids[row] != seq) atomicOr(p.fault, FAULT_BAD_SEQ);
-      else if (pos < 0 || pos >= len) atomicOr(p.fault, FAULT_BAD_POSITION);
-    }
-    int32_t first = dc.n_tiles;
-    for (int j = 0; j < p.q_len; ++j) {
-      const int32_t row = b * p.q_len + j;
-      const int32_t pos = p.app_pos[row];
-      if (p.app_seq_ids[row] == seq && pos >= tok0 && pos < tok_end) first = min(first, (pos - tok0) / kTile);
-    }
-    if (first < dc.n_tiles) dc.app_mode = first < NS - 1 ? 1 : 2;
+  // ---- prologue loads, issued together so their latencies overlap: the
+  // partition's page ids, this entry's appended-row positions and the query
+  // rows (each of them needs only the entry and partition located above)
+  make_plan<D, kSmall, kKReg>(dc.plan, g, lane);
+  dc.PB = page_bytes(g);
+  dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
+  // The partition's page ids, one per lane (partitions start on a page
+  // boundary and span at most 64 pages); bad entries are reported and
+  // replaced by page 0 so every copy stays inside the pool.
+  dc.pg_first = tok0 / g.page_tokens;
+  const int32_t npg = tok_end > tok0 ? (tok_end - 1) / g.page_tokens - dc.pg_first + 1 : 0;
+  int32_t pid = lane < npg ? p.bt[(int64_t)seq * p.bt_stride + dc.pg_first + lane] : 0;
+  // rows appended by this launch (q_len <= 4 per entry)
+  const bool appending = p.app_k != nullptr;
+  int32_t app_pos[4], app_seq[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool in = appending && j < p.q_len;
+    app_pos[j] = in ? p.app_pos[b * p.q_len + j] : -1;
+    app_seq[j] = in ? p.app_seq_ids[b * p.q_len + j] : -1;
   }
 
   const int32_t q_per_kv = p.q_heads / g.kv_heads;
@@ -1128,6 +1131,30 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
                        dc.qhi[nt], dc.qmd[nt], dc.qlo[nt], qmul[nt]);
   }
 
+  if (pid < 0 || pid >= g.num_pages) {
+    atomicOr(p.fault, FAULT_BAD_PAGE);
+    pid = 0;
+  }
+  dc.pidv = pid;
+
+  // ---- rows appended by this launch: checked once per batch entry; written
+  // by the partition that holds their position, before its copies read them
+  dc.app_mode = 0;
+  if (appending) {
+    if (part == 0 && kvh == 0 && lane == 0) {
+      for (int j = 0; j < p.q_len; ++j) {
+        if (app_seq[j] != seq) atomicOr(p.fault, FAULT_BAD_SEQ);
+        else if (app_pos[j] < 0 || app_pos[j] >= len) atomicOr(p.fault, FAULT_BAD_POSITION);
+      }
+    }
+    int32_t first = dc.n_tiles;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (app_seq[j] == seq && app_pos[j] >= tok0 && app_pos[j] < tok_end)
+        first = min(first, (app_pos[j] - tok0) / kTile);
+    if (first < dc.n_tiles) dc.app_mode = first < NS - 1 ? 1 : 2;
+  }
+
   // ---- per-lane softmax rows: PV n-tile np, column li -> row 16*np + li ---
 #pragma unroll
   for (int np = 0; np < NP; ++np) {
@@ -1150,23 +1177,6 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     dc.lrun[np] = 0.0f;
 #pragma unroll
     for (int m = 0; m < D / 16; ++m) dc.oacc[np][m] = v4f{0.f, 0.f, 0.f, 0.f};
-  }
-
-  make_plan<D, kSmall, kKReg>(dc.plan, g, lane);
-  dc.PB = page_bytes(g);
-  dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
-  // The partition's page ids, one per lane (partitions start on a page
-  // boundary and span at most 64 pages); bad entries are reported and
-  // replaced by page 0 so every copy stays inside the pool.
-  dc.pg_first = tok0 / g.page_tokens;
-  {
-    const int32_t npg = tok_end > tok0 ? (tok_end - 1) / g.page_tokens - dc.pg_first + 1 : 0;
-    int32_t pid = lane < npg ? p.bt[(int64_t)seq * p.bt_stride + dc.pg_first + lane] : 0;
-    if (pid < 0 || pid >= g.num_pages) {
-      atomicOr(p.fault, FAULT_BAD_PAGE);
-      pid = 0;
-    }
-    dc.pidv = pid;
   }
 
   dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);

@@ -201,10 +201,9 @@ struct CombineLaunch {
 };
 hipError_t launch_combine(const CombineLaunch &c, hipStream_t s);
 
-// Combine of the flat partials layout written by a decode launch.
-// Blocks (row, entry, split): split s merges partitions [chunk*s,
-// chunk*(s+1)) of the entry; with more than one split a second kernel merges
-// the splits' results (kept in split_ml / split_o).
+// Combine of the flat partials layout written by a decode launch: `slices`
+// 256-thread blocks per (row, entry), each merging all of the entry's
+// partitions (from the header the decode wrote) for head_dim/slices dims.
 struct FlatCombineLaunch {
   const float *ml;
   const float *o;
@@ -215,10 +214,7 @@ struct FlatCombineLaunch {
   int32_t kv_heads;
   int32_t head_dim;
   int32_t n_wg;
-  int32_t splits;    // grid.z: upper bound of ceil(partitions of an entry / chunk)
-  int32_t chunk;     // partitions per split
-  float *split_ml;   // [batch][rows][splits][2]
-  float *split_o;    // [batch][rows][splits][head_dim]
+  int32_t slices;    // blocks per (row, entry), each merging head_dim/slices dims; a power of two
   void *out;
   int32_t out_bf16;
 };

@@ -568,13 +568,14 @@ int32_t batch_rows_per_kv(const rkv_kv_geometry *g, const rkv_decode_args *a) {
 //   header   int32 [1 + 2*batch]: partition length; first partition and
 //            partition count of every entry (written by the decode)
 //   partials f32 (m, l) then o of every (kv head, partition, row)
-//   splits   f32 (m, l) then o of every (entry, row, combine split)
 // Everything is written before it is read in the same call, so the
-// workspace needs no initialisation.
+// workspace needs no initialisation.  Every part grows with batch and
+// max_seq_len: a workspace sized for the largest call of a serving loop
+// holds every smaller one.
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
 struct WsLayout {
-  size_t hdr = 0, ml = 0, o = 0, sml = 0, so = 0, total = 0;
-  int32_t splits = 1, chunk = 1;
+  size_t hdr = 0, ml = 0, o = 0, total = 0;
+  int32_t combine_slices = 1;
 };
 WsLayout ws_layout(const rkv_kv_geometry *g, const rkv_decode_args *a, const Plan &pl) {
   WsLayout w;
@@ -592,23 +593,15 @@ WsLayout ws_layout(const rkv_kv_geometry *g, const rkv_decode_args *a, const Pla
     n_entry = std::min(n_entry, std::max(by_target, (pl.max_len + longest - 1) / longest));
   }
   n_entry = std::min<int64_t>(n_entry, pl.n_wg);
-  // Combine splits: up to 256 (row, entry, split) blocks to keep the CUs
-  // busy when the batch has few rows, else one split per row; a split holds
-  // at least 16 partitions.  rows * splits <= max(rows, 256), and the split
-  // area is reserved at that bound, so every part of the layout grows with
-  // batch and max_seq_len: a workspace sized for the largest call of a
-  // serving loop holds every smaller one.
-  const int64_t blocks = std::max<int64_t>(1, (int64_t)out_rows);
-  const int64_t want = std::max<int64_t>(1, 256 / blocks);
-  const int64_t max_splits = std::max<int64_t>(1, (n_entry + 15) / 16);
-  w.splits = (int32_t)std::min(want, max_splits);
-  w.chunk = (int32_t)std::max<int64_t>(1, (n_entry + w.splits - 1) / w.splits);
-  const size_t split_rows = std::max<size_t>(out_rows, 256);
+  // Combine blocks: (row, entry) times a power-of-two count of dimension
+  // slices, enough for about 512 blocks when partition lists are long (at
+  // most 16 partitions and 256 rows take one slice: one thread per dim).
+  if (n_entry > 16 || out_rows < 256)
+    while (out_rows * w.combine_slices < 512 && g->head_dim / w.combine_slices > 16)
+      w.combine_slices *= 2;
   w.ml = align256(sizeof(int32_t) * (1 + 2 * B));
   w.o = w.ml + align256(sizeof(float) * 2 * prows);
-  w.sml = w.o + align256(sizeof(float) * prows * g->head_dim);
-  w.so = w.sml + align256(sizeof(float) * 2 * split_rows);
-  w.total = w.so + sizeof(float) * split_rows * g->head_dim;
+  w.total = w.o + sizeof(float) * prows * g->head_dim;
   return w;
 }
 size_t ws_bytes(const rkv_kv_geometry *g, const rkv_decode_args *a, const Plan &pl) {
@@ -1038,11 +1031,9 @@ rkv_status decode_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
     if (a->split_event && (e = hipEventRecord(static_cast<hipEvent_t>(a->split_event), hs)) != hipSuccess)
       return hip_fail(op, e);
     const WsLayout w = ws_layout(g, a, pl);
-    uint8_t *base = static_cast<uint8_t *>(a->workspace);
-    rkv::FlatCombineLaunch c{d.ws_ml, d.ws_o, d.ws_hdr, a->batch, a->q_len, a->q_heads,
-                             g->kv_heads, g->head_dim, pl.n_wg, w.splits, w.chunk,
-                             reinterpret_cast<float *>(base + w.sml),
-                             reinterpret_cast<float *>(base + w.so), a->out, d.out_bf16};
+    rkv::FlatCombineLaunch c{d.ws_ml,       d.ws_o,       d.ws_hdr,          a->batch,
+                             a->q_len,      a->q_heads,   g->kv_heads,       g->head_dim,
+                             pl.n_wg,       w.combine_slices, a->out,        d.out_bf16};
     if ((e = rkv::launch_combine_flat(c, hs)) != hipSuccess) return hip_fail(op, e);
   }
   return RKV_OK;

@@ -181,19 +181,21 @@ def test_append_bitexact(rkv, rko, ctx, D, PT, rule, bf16):
                 assert np.array_equal(got[h], want), f"seq {b} kind {kind} head {h}"
 
 
-@pytest.mark.parametrize("D,PT,order", [
-    (256, 64, "chunks"), (256, 64, "shuffled"), (128, 16, "interleaved"), (256, 32, "bad_rows"),
-    (128, 128, "chunks"), (256, 16, "shuffled")])
-def test_append_row_orders(rkv, rko, ctx, D, PT, order):
-    """The append kernel quantizes 32 input rows per workgroup and writes 4
-    aligned consecutive slots of a page with one store: the page bytes equal
-    the oracle's for rows in any order -- chunks starting mid-tile, shuffled
-    rows, two sequences interleaved row by row, and invalid rows inside a
-    group (reported, nothing written for them)."""
+@pytest.mark.parametrize("D,PT,order,big", [
+    (256, 64, "chunks", False), (256, 64, "shuffled", False), (128, 16, "interleaved", False),
+    (256, 32, "bad_rows", False), (128, 128, "chunks", False), (256, 16, "shuffled", False),
+    # >= 32768 rows x 2 kv heads: the 32-row workgroups
+    (256, 64, "shuffled", True), (128, 32, "chunks", True)])
+def test_append_row_orders(rkv, rko, ctx, D, PT, order, big):
+    """The append kernel quantizes 8 or 32 input rows per workgroup and
+    writes 4 aligned consecutive slots of a page with one store: the page
+    bytes equal the oracle's for rows in any order -- chunks starting
+    mid-tile, shuffled rows, two sequences interleaved row by row, and
+    invalid rows inside a group (reported, nothing written for them)."""
     torch = _torch()
     Hkv = 2
-    rng = np.random.default_rng(D + PT + len(order))
-    lens = [700, 413, 97]
+    rng = np.random.default_rng(D + PT + len(order) + big)
+    lens = [20000, 13000, 5003] if big else [700, 413, 97]
     npg = [(L + PT - 1) // PT for L in lens]
     num_pages = sum(npg) + 5
     perm = rng.permutation(num_pages).astype(np.int32)
@@ -206,7 +208,8 @@ def test_append_row_orders(rkv, rko, ctx, D, PT, order):
     sid = np.concatenate([np.full(L, b, np.int32) for b, L in enumerate(lens)])
     pos = np.concatenate([np.arange(L, dtype=np.int32) for L in lens])
     if order == "chunks":      # prefill-like chunks starting at unaligned positions
-        cuts = [0, 13, 77, 300, 301, 700, 700 + 5, 700 + 413, len(sid)]
+        L0, L1 = lens[0], lens[1]
+        cuts = sorted({0, 13, 77, 300, 301, L0, L0 + 5, L0 + L1, len(sid)})
         idx = np.concatenate([np.arange(cuts[i], cuts[i + 1]) for i in rng.permutation(len(cuts) - 1)])
     elif order == "interleaved":
         a, b2 = np.arange(0, 413), np.arange(700, 700 + 413)
