@@ -277,8 +277,11 @@ struct Decoder {
   int lane, li, lg, kvh, b, wave;
   int32_t seq, len, tok0, tok_end, n_tiles;
   int32_t app_mode;        // 0: no rows to append here; 1: before the first copy; 2: after the prologue copies
+  int32_t app_first;       // first tile of this partition that holds an appended row
   int32_t pg_first;        // first page index (within the sequence) of the partition
   int32_t pidv;            // lane i: page id of the partition's i-th page
+  uint64_t pid_bad;        // lanes whose page id was out of range (replaced by page 0)
+  int32_t apos[4];         // positions of this entry's appended rows (-1: another sequence)
   const __attribute__((address_space(3))) int32_t *pg_lds;  // kPageList: page id of page index i
   lds_u8 *vf16;            // kF16V: [dim][4 k-groups] x 8 f16, k-group slot lg ^ (dim & 3)
   const uint8_t *kv_base;  // pages + kv head offset
@@ -369,6 +372,75 @@ struct Decoder {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
+  // kKReg (one wave): the appended rows are handled in two halves around
+  // tile 0's copies.  app_load loads the source values of this partition's
+  // rows (row j is live when its position lies in [tok0, tok_end) on a valid
+  // page); app_store quantizes and stores them, with the page id taken from
+  // pidv.  Neither reloads positions or page ids, so the loads ride with the
+  // prologue's and no dependent round trip follows tile 0's copies.
+  __device__ __forceinline__ void app_load(uint4 (&w)[4][D / 128], bool (&live)[4]) {
+    const Geo &g = p.g;
+    const bool bf16 = p.app_bf16 != 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t pos = apos[j];
+      live[j] = pos >= tok0 && pos < tok_end &&
+                !((pid_bad >> (pos / g.page_tokens - pg_first)) & 1u);
+      if (!live[j]) continue;
+      const int32_t row = b * p.q_len + j;
+#pragma unroll
+      for (int pass = 0; pass < D / 128; ++pass) {
+        const int u = 64 * pass + lane;
+        const int kind = u / (D / 4);
+        const int blk = (u % (D / 4)) >> 3;
+        const int sub = u & 7;
+        const uint64_t off = ((uint64_t)row * g.kv_heads + kvh) * D + (uint64_t)(32 * blk + 4 * sub);
+        const void *src = kind == 0 ? p.app_k : p.app_v;
+        // raw words only: the values are converted in app_store, so no wait
+        // follows a load here
+        if (bf16) {
+          const uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(src) + off);
+          w[j][pass] = uint4{v.x, v.y, 0u, 0u};
+        } else {
+          w[j][pass] = *reinterpret_cast<const uint4 *>(static_cast<const float *>(src) + off);
+        }
+      }
+    }
+  }
+  __device__ __forceinline__ void app_store(const uint4 (&w)[4][D / 128], const bool (&live)[4]) {
+    const Geo &g = p.g;
+    const bool bf16 = p.app_bf16 != 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (!live[j]) continue;
+      const int32_t pos = apos[j];
+      const int32_t page = __builtin_amdgcn_readlane(pidv, pos / g.page_tokens - pg_first);
+      const int32_t slot = pos % g.page_tokens;
+#pragma unroll
+      for (int pass = 0; pass < D / 128; ++pass) {
+        const int u = 64 * pass + lane;
+        const int kind = u / (D / 4);
+        const int blk = (u % (D / 4)) >> 3;
+        const int sub = u & 7;
+        float v[4];
+        if (bf16) {
+          v[0] = bf16_bits_to_f32((uint16_t)(w[j][pass].x & 0xffffu));
+          v[1] = bf16_bits_to_f32((uint16_t)(w[j][pass].x >> 16));
+          v[2] = bf16_bits_to_f32((uint16_t)(w[j][pass].y & 0xffffu));
+          v[3] = bf16_bits_to_f32((uint16_t)(w[j][pass].y >> 16));
+        } else {
+          v[0] = __uint_as_float(w[j][pass].x);
+          v[1] = __uint_as_float(w[j][pass].y);
+          v[2] = __uint_as_float(w[j][pass].z);
+          v[3] = __uint_as_float(w[j][pass].w);
+        }
+        uint16_t scale;
+        const uint32_t codes = q8_quantize_lane(v, p.app_rule, scale);
+        store_q8_lane(g, p.pages_w + region_base(g, page, kvh, kind), kind, slot, blk, sub, codes, scale);
+      }
+    }
+  }
+
   // kKReg: K codes of tile `tile` into kreg.  Lane (li, lg) of M-tile mt
   // holds token row 16*mt + li: dims 64*c + 16*lg .. +15 of 64-dim step c,
   // or (kWide) dims 32*blk + 8*lg .. +7 of block blk.
@@ -388,7 +460,10 @@ struct Decoder {
 
   // Scores, online softmax and PV for the tile held in LDS stage `st`
   // (kKReg: the next tile is copied into `next_stage` meanwhile).
-  __device__ __forceinline__ void compute(int tile, const lds_u8 *st, lds_u8 *next_stage = nullptr) {
+  // drain: wait for this wave's stores before the next tile's copies (the
+  // appended rows of that tile were stored during this one)
+  __device__ __forceinline__ void compute(int tile, const lds_u8 *st, lds_u8 *next_stage = nullptr,
+                                         bool drain = false) {
     const int32_t t0 = tok0 + tile * kTile;
     // ---- QK^T: int32 block dots, scaled by the f16 K scale of (token, block) ----
     // Each plane set computes t = 128*dot(hi) + dot(md) + floor(dot(lo)/128):
@@ -461,6 +536,7 @@ struct Decoder {
     // it.)
     if constexpr (kKReg) {
       if (tile + 1 < n_tiles) {
+        if (drain) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         issue(tile + 1, next_stage);
         load_k(tile + 1);
       }
@@ -689,6 +765,35 @@ struct Decoder {
   // vmcnt waits above instead of draining every copy.
   __device__ __forceinline__ void run(lds_u8 *__restrict__ s0, lds_u8 *__restrict__ s1,
                                       lds_u8 *__restrict__ s2) {
+    if constexpr (kKReg) {
+      // The appended rows' source values are loaded first, with the
+      // prologue's loads still landing.  Position in tile 0 (app_mode 1):
+      // they are quantized and stored, and the stores complete, before tile
+      // 0's copies are issued.  Later tiles (app_mode 2): tile 0 is peeled
+      // off the loop and they are stored after its wait, before its compute;
+      // the vmcnt(0) of step 1 drains them before tile 2's copies, and a
+      // drain in compute(0) precedes tile 1's when a row lies there.
+      uint4 av[4][D / 128];
+      bool alive[4] = {false, false, false, false};
+      if (app_mode != 0) app_load(av, alive);
+      if (app_mode == 1) {
+        app_store(av, alive);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+      if (n_tiles == 0) return;
+      issue(0, s0);
+      load_k(0);
+      __builtin_amdgcn_s_waitcnt(kWaitBase);
+      if (app_mode == 2) app_store(av, alive);
+      compute(0, s0, s1, app_mode == 2 && app_first == 1);
+      int t = 1;
+      for (; t + 1 < n_tiles; t += 2) {
+        step(t, s1, s0);
+        step(t + 1, s0, s1);
+      }
+      if (t < n_tiles) step(t, s1, s0);
+      return;
+    }
     // appended rows are written by wave 0; the other waves copy their tiles
     // only after a barrier that follows the stores
     if (app_mode == 1) {
@@ -698,9 +803,6 @@ struct Decoder {
     if (n_tiles > 0) issue(0, s0);
     if constexpr (NS == 3 && !kKReg) {
       if (n_tiles > 1) issue(1, s1);
-    }
-    if constexpr (kKReg) {
-      if (n_tiles > 0) load_k(0);
     }
     if (app_mode == 2 && wave == 0) append_rows();
     if constexpr (NS == 2) {
@@ -961,17 +1063,11 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
     return e < p.batch ? entry_len(p, sq) : -1;
   };
   const int n_chunks = (p.batch + 63) / 64;
-  // Partitions of a length-L entry at partition length t: ceil(L / t), less
-  // one when the last would hold at most one tile and the one before can
-  // take it within 64 pages (device-chosen lengths only: the per-entry
-  // layout of an explicit length counts ceil(L / t)).  An entry that grew
-  // by this step's token past a multiple of t so keeps its partition count.
-  const bool merge = p.part_tokens == 0;
+  // Partitions of a length-L entry at partition length t: ceil(L / t), the
+  // last one taking the rest.
   auto parts = [&](int32_t L, int32_t t) -> int32_t {
     if (L <= 0) return L < 0 ? 0 : 1;
-    int32_t n = (L + t - 1) / t;
-    if (merge && n > 1 && L - (n - 1) * t <= kTile && t + kTile <= 64 * p.g.page_tokens) --n;
-    return n;
+    return (L + t - 1) / t;
   };
   pt = p.part_tokens;
   if (pt == 0) {
@@ -981,30 +1077,40 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
       for (int c = 0; c < n_chunks; ++c) tot += wave_isum(parts(len_at(c, sq), t), lane);
       return tot;
     };
-    // count(k*unit) >= (sum of ceil((L - kTile)/unit)) / k (a merge drops at
-    // most one tile of an entry), so no k below ceil(that sum / target) can
-    // do: start the search there (exact in one evaluation when the lengths
-    // are equal)
+    // Candidate lengths are whole tiles (pt_unit = 32 tokens), so a
+    // partition may start inside a page and then spans one page more than
+    // its length: a length that is not a multiple of the page must keep
+    // that span within the 64 page ids of a workgroup, else it rounds up to
+    // 64 whole pages.  The rounding keeps the length monotone in k, so the
+    // binary search below stays valid.
+    const int32_t PT = p.g.page_tokens;
+    auto len_of = [&](int32_t k) -> int32_t {
+      const int32_t t = k * p.pt_unit;
+      return (t % PT != 0 && t + PT - kTile > 64 * PT) ? 64 * PT : t;
+    };
+    // count(k*unit) >= (sum of ceil(L/unit)) / k, so no k below
+    // ceil(that sum / target) can do: start the search there (exact in one
+    // evaluation when the lengths are equal)
     int32_t units = 0;
     for (int c = 0; c < n_chunks; ++c) {
-      const int32_t L = len_at(c, sq) - kTile;
+      const int32_t L = len_at(c, sq);
       units += wave_isum(L > 0 ? (L + p.pt_unit - 1) / p.pt_unit : 0, lane);
     }
     const int32_t k0 = (units + p.target_parts - 1) / p.target_parts;
     int32_t lo = max(p.pt_kmin, min(k0, p.pt_kmax)), hi = p.pt_kmax;
-    if (count(lo * p.pt_unit) > p.target_parts) {
-      if (count(hi * p.pt_unit) > p.target_parts) {
+    if (count(len_of(lo)) > p.target_parts) {
+      if (count(len_of(hi)) > p.target_parts) {
         lo = hi;
       } else {
         ++lo;
         while (lo < hi) {
           const int32_t mid = (lo + hi) >> 1;
-          if (count(mid * p.pt_unit) <= p.target_parts) hi = mid;
+          if (count(len_of(mid)) <= p.target_parts) hi = mid;
           else lo = mid + 1;
         }
       }
     }
-    pt = lo * p.pt_unit;
+    pt = len_of(lo);
   }
   int32_t base = 0;
   for (int c = 0; c < n_chunks; ++c) {
@@ -1131,11 +1237,13 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
                        dc.qhi[nt], dc.qmd[nt], dc.qlo[nt], qmul[nt]);
   }
 
-  if (pid < 0 || pid >= g.num_pages) {
+  const bool pid_bad = pid < 0 || pid >= g.num_pages;
+  if (pid_bad) {
     atomicOr(p.fault, FAULT_BAD_PAGE);
     pid = 0;
   }
   dc.pidv = pid;
+  dc.pid_bad = __ballot(pid_bad);
 
   // ---- rows appended by this launch: checked once per batch entry; written
   // by the partition that holds their position, before its copies read them
@@ -1153,6 +1261,9 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
       if (app_seq[j] == seq && app_pos[j] >= tok0 && app_pos[j] < tok_end)
         first = min(first, (app_pos[j] - tok0) / kTile);
     if (first < dc.n_tiles) dc.app_mode = first < NS - 1 ? 1 : 2;
+    dc.app_first = first;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dc.apos[j] = app_seq[j] == seq ? app_pos[j] : -1;
   }
 
   // ---- per-lane softmax rows: PV n-tile np, column li -> row 16*np + li ---

@@ -58,9 +58,11 @@ struct DecodeLaunch {
   float scale_log2;  // softmax scale * log2(e)
   // Partition plan.  part_tokens > 0 fixes the partition length; 0 lets every
   // workgroup derive the same length from the device lengths: the smallest
-  // k*pt_unit, k in [pt_kmin, pt_kmax], whose partition count over the batch
-  // is <= target_parts (else pt_kmax*pt_unit).  Workgroup x of the grid
-  // (n_wg, kv_heads) takes the x-th partition of the batch in entry order.
+  // k*pt_unit (pt_unit = one 32-token tile), k in [pt_kmin, pt_kmax], whose
+  // partition count over the batch is <= target_parts (else the longest);
+  // a length whose partitions could start inside a page and span more than
+  // 64 pages rounds up to 64 pages.  Workgroup x of the grid (n_wg,
+  // kv_heads) takes the x-th partition of the batch in entry order.
   int32_t part_tokens;
   int32_t pt_unit, pt_kmin, pt_kmax, target_parts;
   int32_t max_len;  // >= every length of the batch

@@ -521,9 +521,11 @@ int32_t decode_stages() {
 
 // Partition plan of a decode launch (rkv::DecodeLaunch fields).  Explicit
 // partition_tokens fix the length; 0 leaves it to the kernel, which picks the
-// smallest multiple of max(32, page_tokens), at least 256 tokens and at most
+// smallest whole number of 32-token tiles, at least 256 tokens and at most
 // 64 pages, whose partition count over the batch's actual lengths fills one
-// round of resident workgroups (target = resident slots / kv_heads).
+// round of resident workgroups (target = resident slots / kv_heads).  Tile
+// granularity (not page) keeps the longest partition short: config 2's
+// ragged batch gets 11-tile partitions where whole 64-token pages gave 12.
 struct Plan {
   int32_t pt = 0;  // explicit length, 0 = chosen on the device
   int32_t unit = 0, kmin = 0, kmax = 0, target = 0;
@@ -537,8 +539,8 @@ struct Plan {
 Plan plan_of(const rkv_kv_geometry *g, const rkv_decode_args *a, int32_t stages) {
   Plan pl;
   pl.stages = stages;
-  pl.unit = std::max<int32_t>(32, g->page_tokens);
-  pl.kmin = (256 + pl.unit - 1) / pl.unit;
+  pl.unit = 32;
+  pl.kmin = 256 / pl.unit;
   pl.kmax = 64 * g->page_tokens / pl.unit;
   pl.max_len = std::max<int32_t>(a->max_seq_len, 1);
   const int32_t rows = a->q_len * (a->q_heads / std::max(g->kv_heads, 1));

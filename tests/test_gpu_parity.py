@@ -665,19 +665,27 @@ def _last_rows(sc, b, q_len):
     return sc.k[start:start + q_len], sc.v[start:start + q_len]
 
 
-@pytest.mark.parametrize("Hq,Hkv,D,PT,lens,q_len,part,rule", [
-    (16, 2, 256, 64, [3000, 1000, 64, 2500, 1], 1, 512, 0),
-    (16, 4, 128, 16, [514, 300, 4, 1030], 4, 512, 0),
-    (8, 2, 256, 32, [2049, 33, 40], 2, 1024, 1),
+@pytest.mark.parametrize("Hq,Hkv,D,PT,lens,q_len,part,rule,src_bf16", [
+    # rows in a partition's first tile (len 1), second tile (len 64) and later
+    (16, 2, 256, 64, [3000, 1000, 64, 2500, 1], 1, 512, 0, True),
+    (16, 4, 128, 16, [514, 300, 4, 1030], 4, 512, 0, True),
+    # straddling partitions (2049), tiles 0+1 (33), tile 1 only (40)
+    (8, 2, 256, 32, [2049, 33, 40], 2, 1024, 1, True),
+    # 16 rows per kv head with K codes in registers; f32 source rows
+    (16, 4, 128, 32, [514, 300, 4, 1030, 35], 4, 512, 0, False),
+    # device-chosen partitions (the last partition takes a one-tile remainder)
+    (16, 2, 256, 64, [4097, 66, 300, 12000], 1, 0, 1, False),
 ])
-def test_append_in_decode(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, rule):
+def test_append_in_decode(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, rule, src_bf16):
     """The decode launch's own append (rkv_decode_args.append) writes the same
     bytes as rkv_append_q8 -- also for draft rows that straddle a partition
-    boundary and for rows in a partition's first tile -- and its output equals
-    append-then-decode bit for bit (and the oracle within tolerance)."""
+    boundary and for rows in a partition's first or second tile -- and its
+    output equals append-then-decode bit for bit (and the oracle within
+    tolerance)."""
     torch = _torch()
-    print(f"append-in-decode Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens} q_len={q_len}", flush=True)
-    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=40 + D + q_len, src_bf16=True, rule=rule)
+    print(f"append-in-decode Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens} q_len={q_len} "
+          f"part={part} bf16={src_bf16}", flush=True)
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=40 + D + q_len, src_bf16=src_bf16, rule=rule)
     B = len(lens)
     # the pages the fused path starts from hold junk at the rows it appends
     fused = sc.pages_d.clone()
@@ -689,8 +697,9 @@ def test_append_in_decode(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, rule
     rkv.append_q8(ctx, sc.g, fused, sc.bt_d, rows_sid, pos, junk, -junk)
     kn = np.concatenate([_last_rows(sc, b, q_len)[0] for b in range(B)])
     vn = np.concatenate([_last_rows(sc, b, q_len)[1] for b in range(B)])
-    kd = torch.from_numpy(kn).cuda().to(torch.bfloat16)
-    vd = torch.from_numpy(vn).cuda().to(torch.bfloat16)
+    src_dt = torch.bfloat16 if src_bf16 else torch.float32
+    kd = torch.from_numpy(kn).cuda().to(src_dt)
+    vd = torch.from_numpy(vn).cuda().to(src_dt)
     q = rng.standard_normal((B, q_len, Hq, D)).astype(np.float32)
     q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
     qd = torch.from_numpy(q).cuda().to(torch.bfloat16)
@@ -708,7 +717,7 @@ def test_append_in_decode(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, rule
     assert torch.equal(fused, sc.pages_d), "pages written by the decode's append differ"
     assert np.array_equal(outs[0], outs[1])
     want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(B, dtype=np.int32), q,
-                            scale, part)
+                            scale, part or 1024)
     assert_close(outs[1], want, what="append-in-decode")
 
 
