@@ -64,15 +64,40 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
   const int64_t row0 = (int64_t)blockIdx.x * kAppRows;
   const int nr = (int)min<int64_t>(kAppRows, (int64_t)a.n_rows - row0);
 
-  // ---- rows' destinations (lanes 0-31 of wave 0; the loads of the other
-  // waves' quantize tasks are already in flight meanwhile) ------------------
-  if (tid < 64) {
+  // ---- loads: lanes 0..nr-1 of wave 0 read their row's sequence and
+  // position, then every thread issues its quantize tasks' source loads
+  // (tasks (row, kind, block, lane), lane fastest; dtype and rule fixed at
+  // compile time, rows past the last read as the last row and never
+  // written), all before the first wait; the page lookup that needs the
+  // position follows, so wave 0's critical path is two dependent loads
+  const bool resolver = tid < 64;
+  int32_t seq = -1, pos = -1;
+  if (resolver && tid < nr) {
+    seq = a.seq_ids[row0 + tid];
+    pos = a.positions[row0 + tid];
+  }
+  constexpr int kTasks = kAppRows * 2 * NB * 4;
+  constexpr int kPer = kTasks / 256;
+  static_assert(kTasks % 256 == 0, "every thread takes part in every shuffle round");
+  float v[kPer][8];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int t = 256 * i + tid;
+    const int sub = t & 3;
+    const int blk = (t >> 2) % NB;
+    const int kind = ((t >> 2) / NB) & 1;
+    const int r = min((t >> 2) / NB / 2, nr - 1);
+    load_src8<kBf16>(kind == 0 ? a.k_src : a.v_src,
+                     ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
+                         (uint64_t)(blk * 32 + sub * 8),
+                     v[i]);
+  }
+
+  // ---- rows' destinations (wave 0) --------------------------------------
+  if (resolver) {
     int64_t base = -1;
     int32_t slot = 0;
     if (tid < nr) {
-      const int64_t row = row0 + tid;
-      const int32_t seq = a.seq_ids[row];
-      const int32_t pos = a.positions[row];
       if (seq < 0 || seq >= a.n_seqs) {
         if (kvh == 0) atomicOr(a.fault, FAULT_BAD_SEQ);
       } else if (pos < 0 || pos / g.page_tokens >= a.bt_stride) {
@@ -102,26 +127,7 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
     }
   }
 
-  // ---- quantize: tasks (row, kind, block, lane), lane fastest; fully
-  // unrolled, with dtype and rule fixed at compile time and rows past the
-  // last read as the last row (never written), so every task's source load
-  // is issued before the first wait ------------------------------------------
-  constexpr int kTasks = kAppRows * 2 * NB * 4;
-  constexpr int kPer = kTasks / 256;
-  static_assert(kTasks % 256 == 0, "every thread takes part in every shuffle round");
-  float v[kPer][8];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int t = 256 * i + tid;
-    const int sub = t & 3;
-    const int blk = (t >> 2) % NB;
-    const int kind = ((t >> 2) / NB) & 1;
-    const int r = min((t >> 2) / NB / 2, nr - 1);
-    load_src8<kBf16>(kind == 0 ? a.k_src : a.v_src,
-                     ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
-                         (uint64_t)(blk * 32 + sub * 8),
-                     v[i]);
-  }
+  // ---- quantize into LDS ---------------------------------------------------
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int t = 256 * i + tid;

@@ -620,26 +620,37 @@ struct Decoder {
     // error, exact from an f16 fma, plus (p - f16(p)) * d_v -- and a second
     // MFMA on the same V operand adds it, so the weights are exact to about
     // 2^-22. ----
-    // Tokens past the sequence end may carry junk scales; zero them on the
-    // last tile so 0 * junk cannot turn into NaN.
-    const bool tail = t0 + kTile > len;
-    uint32_t smask[4] = {0xffffffffu, 0xffffffffu, 0xffffffffu, 0xffffffffu};
-    if (tail) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tk = t0 + (i < 2 ? 0 : 16) + 4 * lg + 2 * (i & 1);
-        smask[i] = (tk < len ? 0xffffu : 0u) | (tk + 1 < len ? 0xffff0000u : 0u);
-      }
-    }
-    pv(st, pp, pl, pz, smask);
+    if (t0 + kTile > len) mask_tail_scales(st, t0);
+    pv(st, pp, pl, pz);
   }
 
-  // PV of one tile (see compute); `smask` clears the V scales of tokens past
-  // the sequence end.  (A separate unmasked copy for the other tiles
-  // measured no faster.)
+  // Tokens past the sequence end may carry junk V scales (an f16 NaN or
+  // Inf): the tail tile zeroes them in its landed stage before the PV reads
+  // them, so 0 * junk cannot turn into NaN and no other tile pays for a
+  // mask.  Lane li == 0 of each k-group rewrites the group's 8 scales of
+  // every block; LDS accesses of a wave are performed in order, and the
+  // waves of a workgroup that share the stage write the same values.
+  __device__ __forceinline__ void mask_tail_scales(const lds_u8 *st, int32_t t0) {
+    uint32_t m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int tk = t0 + (i < 2 ? 0 : 16) + 4 * lg + 2 * (i & 1);
+      m[i] = (tk < len ? 0xffffu : 0u) | (tk + 1 < len ? 0xffff0000u : 0u);
+    }
+    if (li != 0) return;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      lds_u8 *a = const_cast<lds_u8 *>(st) + S::kVS + 2 * (blk * 32 + 8 * lg);
+      v4i sv = lds_load<v4i>(a);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[i] = (int)((uint32_t)sv[i] & m[i]);
+      *reinterpret_cast<__attribute__((address_space(3))) v4i *>(a) = sv;
+    }
+  }
+
+  // PV of one tile (see compute).
   __device__ __forceinline__ void pv(const lds_u8 *st, const uint32_t (&pp)[NP][4],
-                                     const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4],
-                                     const uint32_t (&smask)[4]) {
+                                     const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4]) {
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
       // (ext-vector loads only: an LDS load of the uint4 struct type makes the
@@ -647,7 +658,7 @@ struct Decoder {
       const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
       uint32_t sc[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = (uint32_t)sv[i] & smask[i];
+      for (int i = 0; i < 4; ++i) sc[i] = (uint32_t)sv[i];
       v8h pb[NP], pbl[NP];
 #pragma unroll
       for (int np = 0; np < NP; ++np) {
