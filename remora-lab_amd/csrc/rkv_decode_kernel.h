@@ -291,6 +291,7 @@ struct Decoder {
   QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
   float rmul[NP];
   int32_t rlim[NP];
+  int32_t rlim_min;        // the smallest rlim of the live rows (wave-uniform)
   v4f oacc[NP][D / 16];
   float mref[NP], lrun[NP];
 
@@ -471,6 +472,8 @@ struct Decoder {
     // plane's MFMA.  |t| < 2^27, so every step is exact in int32 and the f32
     // conversion rounds once.
     float sacc[kQR][2][4];
+    // tiles wholly below every live row's limit skip the per-token mask
+    const bool full = t0 + kTile <= rlim_min;
 #pragma unroll
     for (int nt = 0; nt < kQR; ++nt)
 #pragma unroll
@@ -570,11 +573,21 @@ struct Decoder {
             // kColSplit: lanes li >= 8 hold row li - 8 (the ror-8 sum is symmetric)
             v = (kColSplit || li < 8 ? lo_t : hi_t) * rmul[np];
           }
-          const int tok = t0 + 16 * mt + 4 * lg + r;
-          const float sv = tok < rlim[np] ? v : -INFINITY;
-          s[4 * mt + r] = sv;
-          tmax = fmaxf(tmax, sv);
+          s[4 * mt + r] = v;
+          tmax = fmaxf(tmax, v);
         }
+      if (!full) {
+        tmax = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int tok = t0 + 16 * mt + 4 * lg + r;
+            const float sv = tok < rlim[np] ? s[4 * mt + r] : -INFINITY;
+            s[4 * mt + r] = sv;
+            tmax = fmaxf(tmax, sv);
+          }
+      }
       tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
       tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
       const bool need = tmax > mref[np] + kTau;  // also true for the first visible tile
@@ -1300,6 +1313,9 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
 #pragma unroll
     for (int m = 0; m < D / 16; ++m) dc.oacc[np][m] = v4f{0.f, 0.f, 0.f, 0.f};
   }
+
+  // rows of draft j attend len - q_len + j + 1 positions; row 0 is live
+  dc.rlim_min = len - p.q_len + 1;
 
   dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
 

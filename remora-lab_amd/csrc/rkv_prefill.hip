@@ -128,6 +128,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
 #pragma unroll
     for (int m = 0; m < D / 16; ++m) dc.oacc[0][m] = v4f{0.f, 0.f, 0.f, 0.f};
   }
+  // chunk token j0 (row 0 of the block) attends the fewest positions
+  dc.rlim_min = jn > 0 ? ctx + j0 + 1 : 0;
   make_plan<D, kSmall>(dc.plan, g, lane);
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
