@@ -395,15 +395,29 @@ def cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv, D, scal
 
 
 def _cpu_model() -> str:
-    """The host CPU's model name (what lscpu prints as "Model name")."""
+    """The host CPU's model name (what lscpu prints as "Model name"), with its
+    family and model numbers and the logical CPU count: a virtual machine may
+    report only the vendor's brand in the name (the GPU boxes say "AMD EPYC";
+    family 26 is Zen 5, 25 is Zen 3/4)."""
+    name, fam, mod = "unknown", None, None
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and name == "unknown":
+                    name = val
+                elif key == "cpu family" and fam is None:
+                    fam = val
+                elif key == "model" and mod is None:
+                    mod = val
+                if name != "unknown" and fam is not None and mod is not None:
+                    break
     except OSError:
         pass
-    return "unknown"
+    extra = [f"family {fam} model {mod}"] if fam is not None and mod is not None else []
+    extra.append(f"{os.cpu_count()} logical CPUs")
+    return f"{name} ({', '.join(extra)})"
 
 
 # ---------------------------------------------------------------------------
