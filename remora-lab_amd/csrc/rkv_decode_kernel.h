@@ -246,7 +246,7 @@ __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "mem
 // the next tile's are loaded as soon as this tile's QK has read them.  The
 // stage then holds only V codes and the scales, 9 KiB at D=256.
 template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kPageList = false,
-          bool kF16V = false, bool kKReg = false>
+          bool kF16V = false, bool kKReg = false, bool kF16K = false>
 struct Decoder {
   using S = StageShape<D, kKReg>;
   static constexpr bool kSplitP = true;    // two-term f16 PV weights (see compute)
@@ -272,6 +272,14 @@ struct Decoder {
   using QOp = typename std::conditional<kWide, int64_t, v4i>::type;
   static constexpr int kQR = kWide ? 1 : NT;   // query operand sets
   static constexpr int kQC = kWide ? NB : NC;  // operands per set and plane
+  // kF16K (the prefill's 8 waves, 16 rows each, bf16 query): the workgroup
+  // widens each tile's K codes to exact f16 once, into kf16, and the QK runs
+  // on v_mfma_f32_16x16x32_f16 against the query as one f16 operand per
+  // block (a bf16 value times a power of two is exact in f16).  Each
+  // (token, row, block) result then costs one K-scale fma instead of the
+  // int8 form's shift, add, convert and fma.
+  static_assert(!kF16K || (kWide && kF16V && !kKReg), "f16 K: 16-row waves that widen V too");
+  static constexpr int kQF = kF16K ? NB : 1;
 
   const DecodeLaunch &p;
   int lane, li, lg, kvh, b, wave;
@@ -289,6 +297,8 @@ struct Decoder {
   ChunkPlan<D, kSmall, kKReg> plan;
   QOp kreg[2][kQC];        // kKReg: K codes of the tile being computed (A operands)
   QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
+  v8h qf[kQF];             // kF16K: query f16 operand per Q8 block (see load_q_f16)
+  lds_u8 *kf16;            // kF16K: [token][D] f16, 16-byte chunk c of row r at c ^ (r & (D/8 - 1))
   float rmul[NP];
   int32_t rlim[NP];
   int32_t rlim_min;        // the smallest rlim of the live rows (wave-uniform)
@@ -480,7 +490,25 @@ struct Decoder {
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sacc[nt][mt][r] = 0.0f;
-    if constexpr (kWide) {
+    if constexpr (kF16K) {
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) {
+        // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
+        const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int krow = 16 * mt + li;
+          // dims 32*blk + 8*lg .. +7 = f16 chunk 4*blk + lg of the row
+          const int pc = (4 * blk + lg) ^ (krow & (D / 8 - 1));
+          const v8h a = lds_load<v8h>(kf16 + krow * (2 * D) + 16 * pc);
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[blk], z, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sacc[0][mt][r] = __builtin_fmaf(c[r], (float)dk8[4 * mt + r], sacc[0][mt][r]);
+        }
+      }
+    } else if constexpr (kWide) {
 #pragma unroll
       for (int blk = 0; blk < NB; ++blk) {
         // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
@@ -764,6 +792,27 @@ struct Decoder {
     }
   }
 
+  // kF16K: widen this wave's share of the landed tile's K codes into kf16.
+  // Physical 16-byte chunk pc of K row r holds logical chunk pc ^ (r mod
+  // D/16), the codes of dims 16*lc .. +15 (signed; xor 0x80 makes them the
+  // biased form v8x4_to_f16 takes).  They become f16 chunks 2*lc and 2*lc+1.
+  __device__ __forceinline__ void widen_k(const lds_u8 *st) {
+    constexpr int kCPR = D / 16;
+    for (int c = wave * 64 + lane; c < 32 * kCPR; c += 64 * NW) {
+      const int r = c / kCPR, pc = c % kCPR;
+      const int lc = pc ^ (r & (kCPR - 1));
+      const v4i w = lds_load<v4i>(st + S::kKC + r * D + 16 * pc);
+      v2h h[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v8x4_to_f16((uint32_t)w[i] ^ 0x80808080u, h[2 * i], h[2 * i + 1]);
+      const v8h f0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+      const v8h f1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+      lds_u8 *row = kf16 + r * (2 * D);
+      *reinterpret_cast<__attribute__((address_space(3))) v8h *>(row + 16 * ((2 * lc) ^ (r & (D / 8 - 1)))) = f0;
+      *reinterpret_cast<__attribute__((address_space(3))) v8h *>(row + 16 * ((2 * lc + 1) ^ (r & (D / 8 - 1)))) = f1;
+    }
+  }
+
   __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
     if constexpr (kKReg) {
       // tile t's K codes and stage copy were the last loads issued
@@ -778,7 +827,8 @@ struct Decoder {
     if (NW > 1) wg_barrier();  // every wave's copies of tile t have landed
     if constexpr (kF16V) {
       widen_v(cur);
-      wg_barrier();  // vf16 holds tile t
+      if constexpr (kF16K) widen_k(cur);
+      wg_barrier();  // vf16 (and kF16K: kf16) hold tile t
     }
     compute(t, cur);
   }
@@ -937,6 +987,53 @@ __device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t
     qmd[c] = v4i{(int)mw[0], (int)mw[1], (int)mw[2], (int)mw[3]};
     qlo[c] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
   }
+}
+
+// The query operand of the f16 QK (kF16K), one v8h per Q8 block: lane
+// (li, lg) serves row li (qbase < 0: a dead row, zeros) with dims
+// 32*b + 8*lg .. +7 of a bf16 query.  The row is scaled by 2^s, s chosen so
+// that amax * 2^s lies in [2^14, 2^15): a bf16 value (8 significant bits)
+// times a power of two is then exact in f16 down to 2^-14, i.e. for every
+// element above amax * 2^-28, and the rest are within amax * 2^-39 of their
+// value.  qmul = scale_log2 * 2^-s undoes the scaling in the softmax.
+template <int D>
+__device__ __forceinline__ void load_q_f16(const uint16_t *qp, int64_t qbase, int lg,
+                                           float scale_log2, v8h *qf, float &qmul) {
+  constexpr int NB = D / 32;
+  float qv[NB][8];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qv[b][e] = 0.0f;
+  if (qbase >= 0) {
+    const uint16_t *q = qp + qbase + 8 * lg;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(q + 32 * b);
+      const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        qv[b][2 * e] = bf16_bits_to_f32((uint16_t)(ws[e] & 0xffffu));
+        qv[b][2 * e + 1] = bf16_bits_to_f32((uint16_t)(ws[e] >> 16));
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[b][e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 16));
+  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  int ex = 0;
+  (void)frexpf(amax, &ex);  // amax = m * 2^ex, m in [0.5, 1)
+  ex = max(ex, -111);       // keeps 2^(15 - ex) finite
+  const float sc = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 0.0f;
+  qmul = amax > 0.0f ? scale_log2 * ldexpf(1.0f, ex - 15) : 0.0f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qf[b][e] = (_Float16)(qv[b][e] * sc);
 }
 
 // The query operands of the 16-row QK (Decoder::kWide): lane (li, lg) holds

@@ -23,14 +23,18 @@
 namespace rkv {
 namespace {
 
-template <int D, bool kSmall, int NS>
+// kQF16: a bf16 query, whose QK runs on f16 MFMA against K codes the
+// workgroup widens once per tile (Decoder kF16K); an f32 query keeps the
+// int8 QK with three query planes.
+template <int D, bool kSmall, int NS, bool kQF16>
 __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_kernel(PrefillLaunch pf) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  using Dec = Decoder<D, 2, kSmall, NS, kPrefillWaves, true, true>;
+  using Dec = Decoder<D, 2, kSmall, NS, kPrefillWaves, true, true, false, kQF16>;
   using S = StageShape<D>;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
   __shared__ int32_t page_list[kPrefillMaxPages];
   __shared__ __attribute__((aligned(16))) uint8_t v_f16[D * 64];  // the tile's V as f16
+  __shared__ __attribute__((aligned(16))) uint8_t k_f16[kQF16 ? D * 64 : 16];  // kQF16: the tile's K as f16
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
@@ -110,6 +114,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.pidv = 0;
   dc.pg_lds = (const __attribute__((address_space(3))) int32_t *)page_list;
   dc.vf16 = (lds_u8 *)v_f16;
+  dc.kf16 = (lds_u8 *)k_f16;
 
   const int32_t G = p.q_heads / g.kv_heads;  // rows of one chunk token
   // row r of the block: chunk token j0 + r / G, q head kvh*G + r % G; the
@@ -120,8 +125,11 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
     const int jl = r / G;
     const int64_t qbase =
         jl < jn ? ((int64_t)(pf.qoff[e] + j0 + jl) * p.q_heads + kvh * G + r % G) * D : -1;
-    load_q_wide<D>(p.q, p.q_bf16 != 0, qbase, lg, p.scale_log2, dc.qhi[0], dc.qmd[0], dc.qlo[0],
-                   dc.rmul[0]);
+    if constexpr (kQF16)
+      load_q_f16<D>(static_cast<const uint16_t *>(p.q), qbase, lg, p.scale_log2, dc.qf, dc.rmul[0]);
+    else
+      load_q_wide<D>(p.q, p.q_bf16 != 0, qbase, lg, p.scale_log2, dc.qhi[0], dc.qmd[0], dc.qlo[0],
+                     dc.rmul[0]);
     dc.rlim[0] = jl < jn ? ctx + j0 + jl + 1 : 0;
     dc.mref[0] = -INFINITY;
     dc.lrun[0] = 0.0f;
@@ -218,10 +226,15 @@ hipError_t launch_prefill_t(const PrefillLaunch &pf, hipStream_t s) {
   const int64_t units = (int64_t)pf.first[pf.n_entries] * pf.d.g.kv_heads;
   const int64_t round = 8 * (int64_t)std::max(pf.xcd_chunk, 1);
   dim3 grid((unsigned)((units + round - 1) / round * round));
-  if (pf.d.g.page_tokens < kTile)
-    hipLaunchKernelGGL((prefill_kernel<D, true, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
+  const bool small = pf.d.g.page_tokens < kTile, qf16 = pf.d.q_bf16 != 0;
+  if (small && qf16)
+    hipLaunchKernelGGL((prefill_kernel<D, true, NS, true>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
+  else if (small)
+    hipLaunchKernelGGL((prefill_kernel<D, true, NS, false>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
+  else if (qf16)
+    hipLaunchKernelGGL((prefill_kernel<D, false, NS, true>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
   else
-    hipLaunchKernelGGL((prefill_kernel<D, false, NS>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
+    hipLaunchKernelGGL((prefill_kernel<D, false, NS, false>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // merge the split entries' partials into their rows

@@ -83,6 +83,9 @@ def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, 
     # G = 1 (128 tokens per block) and G = 16 (8 tokens per block)
     (16, 16, 128, 64, [(10, 150), (0, 7)], True, False, 0.0),
     (32, 2, 128, 128, [(250, 23), (0, 9)], True, False, 0.01),
+    # bf16 q (the f16 QK) on 16-token pages, D = 128 and 256
+    (8, 2, 128, 16, [(0, 33), (200, 100), (31, 2)], True, True, 0.0),
+    (16, 2, 256, 16, [(0, 40), (90, 33), (517, 16)], True, False, 0.01),
 ])
 def test_prefill_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16, out_bf16, outliers):
     lens = [c + n + extra for (c, n), extra in zip(entries, [3, 0, 5, 0, 2])]
