@@ -230,6 +230,11 @@ constexpr float kTau = 4.0f;
 // for every tile copy in flight.  The explicit vmcnt waits order the copies;
 // the "memory" clobber keeps the compiler from moving LDS accesses across.
 __device__ __forceinline__ void wg_barrier() { asm volatile("s_barrier" ::: "memory"); }
+// Barrier after LDS writes that other waves read next: s_barrier does not
+// wait for the wave's outstanding LDS operations, so lgkmcnt(0) first.
+__device__ __forceinline__ void wg_barrier_lds() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // One wave's share of the decode of one (partition, batch entry, kv head).
 // With NW > 1 waves per workgroup, wave w owns query rows 16w .. 16w+15 and
@@ -272,13 +277,15 @@ struct Decoder {
   using QOp = typename std::conditional<kWide, int64_t, v4i>::type;
   static constexpr int kQR = kWide ? 1 : NT;   // query operand sets
   static constexpr int kQC = kWide ? NB : NC;  // operands per set and plane
-  // kF16K (the prefill's 8 waves, 16 rows each, bf16 query): the workgroup
-  // widens each tile's K codes to exact f16 once, into kf16, and the QK runs
-  // on v_mfma_f32_16x16x32_f16 against the query as one f16 operand per
-  // block (a bf16 value times a power of two is exact in f16).  Each
-  // (token, row, block) result then costs one K-scale fma instead of the
-  // int8 form's shift, add, convert and fma.
-  static_assert(!kF16K || (kWide && kF16V && !kKReg), "f16 K: 16-row waves that widen V too");
+  // kF16K (16 rows per wave, bf16 query): the QK runs on
+  // v_mfma_f32_16x16x32_f16 against the query as one f16 operand per block
+  // (a bf16 value times a power of two is exact in f16) and the K codes
+  // widened to exact f16: once per tile by the workgroup into kf16 when it
+  // widens V too (the prefill's 8 waves), else by each wave in registers
+  // (8 codes per operand: two xors, four perms, four packed subtractions).
+  // Each (token, row, block) result then costs one K-scale fma instead of
+  // the int8 form's shift, add, convert and fma.
+  static_assert(!kF16K || kWide, "f16 K: 16-row waves");
   static constexpr int kQF = kF16K ? NB : 1;
 
   const DecodeLaunch &p;
@@ -498,9 +505,21 @@ struct Decoder {
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const int krow = 16 * mt + li;
-          // dims 32*blk + 8*lg .. +7 = f16 chunk 4*blk + lg of the row
-          const int pc = (4 * blk + lg) ^ (krow & (D / 8 - 1));
-          const v8h a = lds_load<v8h>(kf16 + krow * (2 * D) + 16 * pc);
+          v8h a;
+          if constexpr (kF16V) {
+            // dims 32*blk + 8*lg .. +7 = f16 chunk 4*blk + lg of the row
+            const int pc = (4 * blk + lg) ^ (krow & (D / 8 - 1));
+            a = lds_load<v8h>(kf16 + krow * (2 * D) + 16 * pc);
+          } else {
+            // the int8 operand (see the kWide QK below), widened
+            const int pc = (2 * blk + (lg >> 1)) ^ (krow & (S::kCPR - 1));
+            const int64_t k8 = kKReg ? kreg[mt][blk]
+                                     : lds_load<int64_t>(st + S::kKC + krow * D + 16 * pc + 8 * (lg & 1));
+            v2h h0, h1, h2, h3;
+            v8x4_to_f16((uint32_t)k8 ^ 0x80808080u, h0, h1);
+            v8x4_to_f16((uint32_t)((uint64_t)k8 >> 32) ^ 0x80808080u, h2, h3);
+            a = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+          }
           const v4f z = {0.f, 0.f, 0.f, 0.f};
           const v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[blk], z, 0, 0, 0);
 #pragma unroll
@@ -828,7 +847,7 @@ struct Decoder {
     if constexpr (kF16V) {
       widen_v(cur);
       if constexpr (kF16K) widen_k(cur);
-      wg_barrier();  // vf16 (and kF16K: kf16) hold tile t
+      wg_barrier_lds();  // vf16 (and kF16K: kf16) hold tile t
     }
     compute(t, cur);
   }
@@ -1257,14 +1276,17 @@ __device__ __forceinline__ bool locate(const DecodeLaunch &p, int lane, int32_t 
 // NW = 1: one wave per workgroup, NT n-tiles of 8 rows (up to 16 rows).
 // NW = 2: two waves, 16 rows each (NT = 2 per wave, up to 32 rows), two
 // waves per SIMD.
-template <int D, int NT, bool kSmall, int NS, int NW = 1>
+// kQF16: a bf16 query with 16 rows per wave, whose QK runs on f16 MFMA
+// (Decoder kF16K); otherwise the int8 QK with three query planes.
+template <int D, int NT, bool kSmall, int NS, int NW = 1, bool kQF16 = false>
 __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
 #if defined(__HIP_DEVICE_COMPILE__)
   // single-wave workgroups over pages of >= 32 tokens with the two-stage
   // ring take the K codes straight to registers (compute copies tile t+1
   // into the stage tile t-1 used)
   constexpr bool kKReg = NW == 1 && !kSmall && NS == 2;
-  using Dec = Decoder<D, NT, kSmall, NS, NW, false, false, kKReg>;
+  static_assert(!kQF16 || NT == 2, "the f16 QK serves 16-row waves");
+  using Dec = Decoder<D, NT, kSmall, NS, NW, false, false, kKReg, kQF16>;
   using S = typename Dec::S;
   constexpr int NP = Dec::NP;
   constexpr int NC = Dec::NC;
@@ -1348,7 +1370,10 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     return (((int64_t)b * p.q_len + j) * p.q_heads + h) * D;
   };
   float qmul[NT];
-  if constexpr (Dec::kWide) {
+  if constexpr (kQF16) {
+    load_q_f16<D>(static_cast<const uint16_t *>(p.q), qrow(r0 + li), lg, p.scale_log2, dc.qf,
+                  qmul[0]);
+  } else if constexpr (Dec::kWide) {
     load_q_wide<D>(p.q, p.q_bf16 != 0, qrow(r0 + li), lg, p.scale_log2, dc.qhi[0], dc.qmd[0],
                    dc.qlo[0], qmul[0]);
   } else {
@@ -1453,7 +1478,17 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
 template <int D, int NT, int NS, int NW = 1>
 hipError_t launch_decode_t(const DecodeLaunch &d, hipStream_t s) {
   dim3 grid((unsigned)d.n_wg, (unsigned)d.g.kv_heads);
-  if (d.g.page_tokens < kTile)
+  const bool small = d.g.page_tokens < kTile;
+  if constexpr (NT == 2) {
+    if (d.q_bf16 != 0) {
+      if (small)
+        hipLaunchKernelGGL((decode_kernel<D, NT, true, NS, NW, true>), grid, dim3(64 * NW), 0, s, d);
+      else
+        hipLaunchKernelGGL((decode_kernel<D, NT, false, NS, NW, true>), grid, dim3(64 * NW), 0, s, d);
+      return hipGetLastError();
+    }
+  }
+  if (small)
     hipLaunchKernelGGL((decode_kernel<D, NT, true, NS, NW>), grid, dim3(64 * NW), 0, s, d);
   else
     hipLaunchKernelGGL((decode_kernel<D, NT, false, NS, NW>), grid, dim3(64 * NW), 0, s, d);
