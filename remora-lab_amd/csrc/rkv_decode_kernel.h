@@ -287,6 +287,15 @@ struct Decoder {
   // the int8 form's shift, add, convert and fma.
   static_assert(!kF16K || kWide, "f16 K: 16-row waves");
   static constexpr int kQF = kF16K ? NB : 1;
+  // kDSplit (the two-wave verify with a bf16 query, 2-stage ring): wave w
+  // owns half of the head dimension, blocks w*NB/2 .. +NB/2-1, for all 32
+  // rows, and the softmax of its own 16 rows.  Each wave widens and reads
+  // only its half of every K and V tile; the halves' partial scores and
+  // the rows' p values cross through LDS (see compute_split).  qf then holds
+  // [n-tile][own block] and oacc[0] holds [n-tile][own 16-dim tile].
+  static constexpr bool kDSplit = NW == 2 && kF16K && !kF16V && NS == 2;
+  static constexpr int kHB = NB / 2;  // kDSplit: blocks of a wave's half
+  static constexpr int kHM = D / 32;  // kDSplit: 16-dim PV tiles of a wave's half
 
   const DecodeLaunch &p;
   int lane, li, lg, kvh, b, wave;
@@ -306,6 +315,7 @@ struct Decoder {
   QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
   v8h qf[kQF];             // kF16K: query f16 operand per Q8 block (see load_q_f16)
   lds_u8 *kf16;            // kF16K: [token][D] f16, 16-byte chunk c of row r at c ^ (r & (D/8 - 1))
+  lds_u8 *xs;              // kDSplit: partial scores [wave][lane][8] f32, then alphas [wave][lane] f32
   float rmul[NP];
   int32_t rlim[NP];
   int32_t rlim_min;        // the smallest rlim of the live rows (wave-uniform)
@@ -684,6 +694,190 @@ struct Decoder {
     pv(st, pp, pl, pz);
   }
 
+  // kDSplit: tile `tile` (stage `st`) on this wave's half of the dims.
+  //  1. QK of all 32 rows over the half's blocks (f16 MFMA, K widened in
+  //     registers): partial scores of n-tiles 0 and 1.
+  //  2. The other wave's rows' partials go to LDS (slot w of xs); after a
+  //     barrier this wave adds the other half's partials of its own rows.
+  //  3. Online softmax of the own rows (as compute's, one n-tile).
+  //  4. p (two f16 terms) and the rescale factor of the own rows go to LDS
+  //     (p in the stage's K-code area, which the QK no longer needs); after a
+  //     barrier this wave reads the other rows' and rescales their
+  //     accumulators if the other wave moved its maxima.
+  //  5. PV of all 32 rows over the half's dims (V widened in registers).
+  // The wave number is a template argument so that every register array
+  // index below is a constant.
+  __device__ __forceinline__ void compute_split(int tile, const lds_u8 *st) {
+    if (wave == 0) compute_split_w<0>(tile, st);
+    else compute_split_w<1>(tile, st);
+  }
+  template <int W>
+  __device__ __forceinline__ void compute_split_w(int tile, const lds_u8 *st) {
+    const int32_t t0 = tok0 + tile * kTile;
+    const bool full = t0 + kTile <= rlim_min;
+    constexpr int w = W, o = 1 - W;
+    float sacc[2][2][4];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sacc[nt][mt][r] = 0.0f;
+#pragma unroll
+    for (int bl = 0; bl < kHB; ++bl) {
+      const int blk = w * kHB + bl;
+      const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const int krow = 16 * mt + li;
+        const int pc = (2 * blk + (lg >> 1)) ^ (krow & (S::kCPR - 1));
+        const int64_t k8 = lds_load<int64_t>(st + S::kKC + krow * D + 16 * pc + 8 * (lg & 1));
+        v2h h0, h1, h2, h3;
+        v8x4_to_f16((uint32_t)k8 ^ 0x80808080u, h0, h1);
+        v8x4_to_f16((uint32_t)((uint64_t)k8 >> 32) ^ 0x80808080u, h2, h3);
+        const v8h a = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[nt * kHB + bl], z, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sacc[nt][mt][r] = __builtin_fmaf(c[r], (float)dk8[4 * mt + r], sacc[nt][mt][r]);
+        }
+      }
+    }
+
+    // ---- 2. partial-score exchange ----
+    __attribute__((address_space(3))) v4f *ps = reinterpret_cast<__attribute__((address_space(3))) v4f *>(xs);
+    ps[(w * 64 + lane) * 2] = v4f{sacc[o][0][0], sacc[o][0][1], sacc[o][0][2], sacc[o][0][3]};
+    ps[(w * 64 + lane) * 2 + 1] = v4f{sacc[o][1][0], sacc[o][1][1], sacc[o][1][2], sacc[o][1][3]};
+    wg_barrier_lds();
+    const v4f q0 = ps[(o * 64 + lane) * 2], q1 = ps[(o * 64 + lane) * 2 + 1];
+    float sown[2][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      sown[0][r] = sacc[w][0][r] + q0[r];
+      sown[1][r] = sacc[w][1][r] + q1[r];
+    }
+
+    // ---- 3. online softmax of the own rows ----
+    float s[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = sown[mt][r] * rmul[0];
+        s[4 * mt + r] = v;
+        tmax = fmaxf(tmax, v);
+      }
+    if (!full) {
+      tmax = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tok = t0 + 16 * mt + 4 * lg + r;
+          const float sv = tok < rlim[0] ? s[4 * mt + r] : -INFINITY;
+          s[4 * mt + r] = sv;
+          tmax = fmaxf(tmax, sv);
+        }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const bool need = tmax > mref[0] + kTau;  // also true for the first visible tile
+    float alpha = 1.0f;
+    if (__any(need)) {
+      const float mnew = need ? tmax : mref[0];
+      alpha = !need ? 1.0f : (mref[0] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mref[0] - mnew));
+      lrun[0] *= alpha;
+#pragma unroll
+      for (int m = 0; m < kHM; ++m) oacc[0][w * kHM + m] *= alpha;
+      mref[0] = mnew;
+    }
+    const float muse = mref[0] == -INFINITY ? 0.0f : mref[0];
+    float pr[8];
+    float lsum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pr[e] = __builtin_amdgcn_exp2f(s[e] - muse);
+      lsum += pr[e];
+    }
+    lrun[0] += lsum;
+    uint32_t pq[2][8];  // [n-tile][p hi x4, p lo x4]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const v2h h2 = {(_Float16)pr[2 * i], (_Float16)pr[2 * i + 1]};
+      const v2h l2 = {(_Float16)(pr[2 * i] - (float)h2[0]), (_Float16)(pr[2 * i + 1] - (float)h2[1])};
+      pq[w][i] = __builtin_bit_cast(uint32_t, h2);
+      pq[w][4 + i] = __builtin_bit_cast(uint32_t, l2);
+    }
+
+    // ---- 4. p and rescale exchange (p in this stage's K-code area) ----
+    __attribute__((address_space(3))) v4i *px =
+        reinterpret_cast<__attribute__((address_space(3))) v4i *>(const_cast<lds_u8 *>(st) + S::kKC);
+    __attribute__((address_space(3))) float *ax =
+        reinterpret_cast<__attribute__((address_space(3))) float *>(xs + 2 * 64 * 32);
+    px[(w * 64 + lane) * 2] = v4i{(int)pq[w][0], (int)pq[w][1], (int)pq[w][2], (int)pq[w][3]};
+    px[(w * 64 + lane) * 2 + 1] = v4i{(int)pq[w][4], (int)pq[w][5], (int)pq[w][6], (int)pq[w][7]};
+    ax[w * 64 + lane] = alpha;
+    wg_barrier_lds();
+    {
+      const v4i a0 = px[(o * 64 + lane) * 2], a1 = px[(o * 64 + lane) * 2 + 1];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pq[o][i] = (uint32_t)a0[i];
+        pq[o][4 + i] = (uint32_t)a1[i];
+      }
+      const float alpha_o = ax[o * 64 + lane];
+      if (__any(alpha_o != 1.0f)) {
+#pragma unroll
+        for (int m = 0; m < kHM; ++m) oacc[0][o * kHM + m] *= alpha_o;
+      }
+    }
+
+    // ---- 5. PV of all 32 rows over the half's dims ----
+    if (t0 + kTile > len) mask_tail_scales(st, t0);
+#pragma unroll
+    for (int bl = 0; bl < kHB; ++bl) {
+      const int blk = w * kHB + bl;
+      const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
+      v8h pb[2], pbl[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v2h ph = __builtin_bit_cast(v2h, pq[nt][i]);
+          const v2h dv = __builtin_bit_cast(v2h, (uint32_t)sv[i]);
+          const v2h prod = ph * dv;
+          const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
+          const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pq[nt][4 + i]), dv, err);
+          pb[nt][2 * i] = prod[0];
+          pb[nt][2 * i + 1] = prod[1];
+          pbl[nt][2 * i] = lo[0];
+          pbl[nt][2 * i + 1] = lo[1];
+        }
+      }
+#pragma unroll
+      for (int hm = 0; hm < 2; ++hm) {
+        const int d = 32 * blk + 16 * hm + li;
+        const int sw = (d >> 2) & 1;
+        const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * lg);
+        const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * lg);
+        v2h a0, a1, a2, a3;
+        v8x4_to_f16(w0, a0, a1);
+        v8x4_to_f16(w1, a2, a3);
+        const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) {
+          v4f &acc = oacc[0][nt * kHM + 2 * bl + hm];
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[nt], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[nt], acc, 0, 0, 0);
+        }
+      }
+    }
+  }
+
   // Tokens past the sequence end may carry junk V scales (an f16 NaN or
   // Inf): the tail tile zeroes them in its landed stage before the PV reads
   // them, so 0 * junk cannot turn into NaN and no other tile pays for a
@@ -849,7 +1043,8 @@ struct Decoder {
       if constexpr (kF16K) widen_k(cur);
       wg_barrier_lds();  // vf16 (and kF16K: kf16) hold tile t
     }
-    compute(t, cur);
+    if constexpr (kDSplit) compute_split(t, cur);
+    else compute(t, cur);
   }
 
   // The whole tile loop.  The stages are distinct restrict pointers of this
@@ -1015,7 +1210,9 @@ __device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t
 // times a power of two is then exact in f16 down to 2^-14, i.e. for every
 // element above amax * 2^-28, and the rest are within amax * 2^-39 of their
 // value.  qmul = scale_log2 * 2^-s undoes the scaling in the softmax.
-template <int D>
+// kParts > 1: only blocks kPart*NB/kParts .. +NB/kParts-1 go to qf (the
+// scale still follows the whole row).
+template <int D, int kParts = 1, int kPart = 0>
 __device__ __forceinline__ void load_q_f16(const uint16_t *qp, int64_t qbase, int lg,
                                            float scale_log2, v8h *qf, float &qmul) {
   constexpr int NB = D / 32;
@@ -1049,10 +1246,11 @@ __device__ __forceinline__ void load_q_f16(const uint16_t *qp, int64_t qbase, in
   ex = max(ex, -111);       // keeps 2^(15 - ex) finite
   const float sc = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 0.0f;
   qmul = amax > 0.0f ? scale_log2 * ldexpf(1.0f, ex - 15) : 0.0f;
+  constexpr int kNB = NB / kParts;
 #pragma unroll
-  for (int b = 0; b < NB; ++b)
+  for (int b = 0; b < kNB; ++b)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qf[b][e] = (_Float16)(qv[b][e] * sc);
+    for (int e = 0; e < 8; ++e) qf[b][e] = (_Float16)(qv[kPart * kNB + b][e] * sc);
 }
 
 // The query operands of the 16-row QK (Decoder::kWide): lane (li, lg) holds
@@ -1291,8 +1489,11 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   constexpr int NP = Dec::NP;
   constexpr int NC = Dec::NC;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
+  // kDSplit: partial scores [2][64][8] f32, then rescale factors [2][64] f32
+  __shared__ __attribute__((aligned(16))) uint8_t xsbuf[Dec::kDSplit ? 2 * 64 * 32 + 2 * 64 * 4 : 16];
 
   Dec dc(p);
+  dc.xs = (lds_u8 *)xsbuf;
   dc.lane = threadIdx.x & 63;
   dc.wave = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
   const int r0 = 16 * dc.wave;  // first query row of this wave
@@ -1370,7 +1571,19 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     return (((int64_t)b * p.q_len + j) * p.q_heads + h) * D;
   };
   float qmul[NT];
-  if constexpr (kQF16) {
+  if constexpr (Dec::kDSplit) {
+    // all 32 rows (n-tiles 0 and 1) on this wave's half of the blocks; the
+    // softmax scale is the own n-tile's
+    const uint16_t *q16 = static_cast<const uint16_t *>(p.q);
+    constexpr int HB = Dec::kHB;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      float qm;
+      if (dc.wave == 0) load_q_f16<D, 2, 0>(q16, qrow(16 * nt + li), lg, p.scale_log2, &dc.qf[nt * HB], qm);
+      else load_q_f16<D, 2, 1>(q16, qrow(16 * nt + li), lg, p.scale_log2, &dc.qf[nt * HB], qm);
+      if (nt == dc.wave) qmul[0] = qm;
+    }
+  } else if constexpr (kQF16) {
     load_q_f16<D>(static_cast<const uint16_t *>(p.q), qrow(r0 + li), lg, p.scale_log2, dc.qf,
                   qmul[0]);
   } else if constexpr (Dec::kWide) {
@@ -1440,6 +1653,60 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   dc.rlim_min = len - p.q_len + 1;
 
   dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
+
+  if constexpr (Dec::kDSplit) {
+    // o of all 32 rows over this wave's half of the dims; (m, l) of its own
+    // 16 rows.  A direct output needs the other rows' l too: through the
+    // partial-score slots of xs, which the last tile read before its second
+    // barrier.
+    float l = dc.lrun[0];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    float l_other = 0.0f;
+    if (p.ws_o == nullptr) {
+      __attribute__((address_space(3))) float *lx = reinterpret_cast<__attribute__((address_space(3))) float *>(dc.xs);
+      lx[dc.wave * 64 + lane] = l;
+      wg_barrier_lds();
+      l_other = lx[(1 - dc.wave) * 64 + lane];
+    }
+    constexpr int HM = Dec::kHM;
+    const int d_half = dc.wave * (D / 2);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int row = 16 * nt + li;
+      if (row >= R) continue;
+      const bool own = nt == dc.wave;
+      const float lr = own ? l : l_other;
+      const int j = row / q_per_kv;
+      const int h = kvh * q_per_kv + row % q_per_kv;
+      const int64_t orow = ((int64_t)b * p.q_len + j) * p.q_heads + h;
+      if (p.ws_o == nullptr) {
+        const float inv_l = lr > 0.0f ? 1.0f / lr : 0.0f;
+#pragma unroll
+        for (int m = 0; m < HM; ++m) {
+          const int d0 = d_half + 16 * m + 4 * lg;
+          const v4f o = lr > 0.0f ? dc.oacc[0][nt * HM + m] * inv_l : v4f{0.f, 0.f, 0.f, 0.f};
+          if (p.out_bf16 != 0) {
+            uint16_t *dst = static_cast<uint16_t *>(p.out) + orow * D + d0;
+            const uint32_t w0 = (uint32_t)f32_to_bf16_rtne(o[0]) | ((uint32_t)f32_to_bf16_rtne(o[1]) << 16);
+            const uint32_t w1 = (uint32_t)f32_to_bf16_rtne(o[2]) | ((uint32_t)f32_to_bf16_rtne(o[3]) << 16);
+            *reinterpret_cast<uint2 *>(dst) = uint2{w0, w1};
+          } else {
+            *reinterpret_cast<v4f *>(static_cast<float *>(p.out) + orow * D + d0) = o;
+          }
+        }
+      } else {
+        const int64_t prow = p.ws_hdr != nullptr
+                                 ? ((int64_t)kvh * p.n_wg + (int64_t)blockIdx.x) * R + row
+                                 : orow * p.n_parts + part;
+#pragma unroll
+        for (int m = 0; m < HM; ++m)
+          *reinterpret_cast<v4f *>(p.ws_o + prow * D + d_half + 16 * m + 4 * lg) = dc.oacc[0][nt * HM + m];
+        if (own && lg == 0) *reinterpret_cast<float2 *>(p.ws_ml + 2 * prow) = float2{dc.mref[0], l};
+      }
+    }
+    return;
+  }
 
   // ---- epilogue ---------------------------------------------------------------
   if constexpr (Dec::kColSplit) {

@@ -487,6 +487,41 @@ def test_splitk_partials_and_combine(rkv, rko, ctx):
     assert_close(direct, want, what="combine")
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,PT,lens,q_len,part,out_bf16", [
+    # D = 128, device-chosen partitions
+    (16, 2, 128, 64, [700, 33, 1], 4, 0, False),
+    # 16-token pages, bf16 out
+    (16, 2, 256, 16, [300, 40], 4, 0, True),
+    # 24 rows per kv head (8 dead rows in the second wave's n-tile); every
+    # length <= 256: one partition, direct (normalized) output
+    (16, 2, 256, 64, [200, 100, 7], 3, 0, False),
+    # explicit partitions, bf16 out
+    (32, 4, 256, 32, [900, 129], 4, 512, True),
+])
+def test_verify_bf16_query_shapes(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, out_bf16):
+    """17..32 rows per kv head with a bf16 query: the two waves split the head
+    dimension (f16 QK on widened K codes, partial scores and p exchanged
+    through LDS).  Against the oracle, across head sizes, page sizes, dead
+    rows, the direct output and the split-K partials."""
+    print(f"verify bf16 Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens} q_len={q_len} part={part}", flush=True)
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=5 * D + PT + q_len, src_bf16=True, outliers=0.01)
+    rng = np.random.default_rng(D + q_len + PT)
+    q = outlier_q(rng, (len(lens), q_len, Hq, D))
+    q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    scale = 1.0 / math.sqrt(D)
+    got, pt = _run_decode(rkv, ctx, sc, q, scale, q_bf16=True, q_len=q_len, partition_tokens=part,
+                          out_bf16=out_bf16)
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(len(lens), dtype=np.int32),
+                            q, scale, pt)
+    if out_bf16:
+        # the f32 result rounded once to bf16 (half an ulp = 2^-9 relative)
+        err = np.abs(got - want) - np.abs(want) * 2.0 ** -8
+        assert float(err.max()) <= ATOL
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) <= RTOL + 2.0 ** -8
+    else:
+        assert_close(got, want, what="verify bf16 q")
+
+
 def test_verify_causal(rkv, rko, ctx):
     """q_len=4 causal verify: draft row j attends positions [0, ctx+j]; equal to
     the oracle and to single-row decodes of length ctx+j+1 (attention.rs:169-215)."""
