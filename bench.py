@@ -252,7 +252,7 @@ def main() -> int:
                       "sampled_steps": len(sampled), "sampled_every": args.event_every},
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
-        "roofline": {"bound": "hbm", "kernel": "rkv::decode_kernel<256, 1, false, 2, 1>",
+        "roofline": {"bound": "hbm", "kernel": "rkv::decode_kernel<256, 1, false, 2, 1, false>",
                      "achieved": round(dec_bytes / dec_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic(), "algorithmic_bytes_per_launch": dec_bytes},
