@@ -1,7 +1,8 @@
 """Seeded random shapes through the decode/verify and prefill paths against
 the oracle: batch size, lengths (0, 1, page and tile edges included), GQA,
 head_dim, page size, q_len 1..4, explicit or device-chosen partitions,
-f32/bf16 q, appended rows.  Each case is fixed by its seed, so a failure
+f32/bf16 q (the bf16 query takes the f16 QK with 16 or 32 rows per kv head
+and in the prefill), appended rows.  Each case is fixed by its seed, so a failure
 names a reproducible shape.  Bars as in test_gpu_parity.py."""
 import math
 
@@ -62,12 +63,18 @@ def test_random_prefill_shapes(rkv, rko, ctx, seed):
     Hq = Hkv * G
     n_ent = int(rng.integers(1, 5))
     ents = [(int(rng.integers(0, 600)), int(rng.integers(1, 200))) for _ in range(n_ent)]
-    print(f"seed {seed}: D={D} PT={PT} Hkv={Hkv} Hq={Hq} entries={ents}", flush=True)
+    print(f"seed {seed}: D={D} PT={PT} Hkv={Hkv} Hq={Hq} entries={ents}", flush=True)  # q dtype below
     lens = [c + n for c, n in ents]
     sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=seed, src_bf16=True)
     total = sum(n for _, n in ents)
     q = rng.standard_normal((total, Hq, D)).astype(np.float32)
+    # drawn last so the shapes above stay those of the f32-only cases
+    q_bf16 = bool(rng.random() < 0.5)
+    if q_bf16:
+        q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
     qd = torch.from_numpy(q).cuda()
+    if q_bf16:
+        qd = qd.to(torch.bfloat16)
     out = torch.full((total, Hq, D), float("nan"), device="cuda")
     a = rkv.prefill_args(list(range(n_ent)), [c for c, _ in ents], [n for _, n in ents], qd, out,
                          1.0 / math.sqrt(D))
