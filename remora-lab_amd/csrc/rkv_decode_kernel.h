@@ -292,8 +292,9 @@ struct Decoder {
   // rows, and the softmax of its own 16 rows.  Each wave widens and reads
   // only its half of every K and V tile; the halves' partial scores and
   // the rows' p values cross through LDS (see compute_split).  qf then holds
-  // [n-tile][own block] and oacc[0] holds [n-tile][own 16-dim tile].
-  static constexpr bool kDSplit = NW == 2 && kF16K && !kF16V && NS == 2;
+  // [n-tile][own block] and oacc[0] holds [n-tile][own 16-dim tile].  Not on
+  // 16-token pages: their copy plan leaves the split too few registers.
+  static constexpr bool kDSplit = NW == 2 && kF16K && !kF16V && NS == 2 && !kSmall;
   static constexpr int kHB = NB / 2;  // kDSplit: blocks of a wave's half
   static constexpr int kHM = D / 32;  // kDSplit: 16-dim PV tiles of a wave's half
 
@@ -321,8 +322,96 @@ struct Decoder {
   int32_t rlim_min;        // the smallest rlim of the live rows (wave-uniform)
   v4f oacc[NP][D / 16];
   float mref[NP], lrun[NP];
+  // The PV weights multiply the V scales times 2^vexp (see scale_v), so
+  // oacc carries that factor; finish() divides it out.
+  static constexpr int32_t kVexpMax = 30;
+  int32_t vexp = kVexpMax;
+  lds_u8 *vsc;             // NW > 1: this wave's 2*D-byte copy of the tile's scaled V scales
 
   __device__ __forceinline__ Decoder(const DecodeLaunch &p_) : p(p_) {}
+
+  // The V scales of the tile in stage `st` times 2^vexp, for the PV: in
+  // place with one wave (its LDS accesses are performed in order), else in
+  // this wave's copy vsc (the waves of a workgroup share the stage).
+  // The PV weights are f16 products p * d_v (two terms, see compute).  With
+  // the scales as stored, a V of small magnitude (d_v below about 2^-12,
+  // |v| below about 0.03) puts them in the f16 subnormal range, whose
+  // absolute spacing 2^-24 is far coarser than the two terms carry.  vexp
+  // is the largest exponent with 2^vexp * max d_v <= 2^11 over the
+  // partition's tiles so far (0 <= d_v; the maximum's f16 exponent field e
+  // gives d_v < 2^(e-14), so vexp = 25 - max(e, 1), at most kVexpMax): a
+  // power-of-two step that is exact, keeps every weight below 2^15 (p <=
+  // 2^kTau) and every weight of a p >= 2^-25 on the tile's largest scale
+  // normal.  vexp only decreases; when it does, the accumulators take the
+  // same exact step.  probe_v reads the scales and tests them against the
+  // current vexp (each lane its own: a few instructions per tile); only a
+  // tile that needs a smaller vexp (a partition's first, then rarely) takes
+  // apply_v's wave-wide maximum and the accumulators' step.  Split so that
+  // a tile's QK can hide the probe's latency.
+  static constexpr int kVW = D / 128;  // 32-bit words of the tile's 2*D bytes of V scales per lane
+  struct VProbe {
+    uint32_t w[kVW];  // the lane's scales, as stored
+    int32_t mx;       // their largest |d_v| bit pattern
+  };
+  __device__ __forceinline__ bool probe_v(const lds_u8 *st, VProbe &v) const {
+    const lds_u8 *src = st + S::kVS + 4 * kVW * lane;
+    uint32_t mx = 0;
+#pragma unroll
+    for (int i = 0; i < kVW; ++i) {
+      v.w[i] = lds_load<uint32_t>(src + 4 * i);
+      const uint32_t a = v.w[i] & 0x7fff7fffu;  // |d_v| as u16 pairs: ordered as the values
+      mx = max(mx, max(a & 0xffffu, a >> 16));
+    }
+    v.mx = (int32_t)mx;
+    // exponent field e > 25 - vexp: this vexp would take a weight past 2^15
+    return v.mx >= (26 - vexp) * 1024;
+  }
+  __device__ __forceinline__ const lds_u8 *apply_v(const lds_u8 *st, bool over, const VProbe &v) {
+    if (__any(over)) {
+      int32_t m = v.mx;
+      m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x111, 0xf, 0xf, false));  // row_shr:1
+      m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x112, 0xf, 0xf, false));  // row_shr:2
+      m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x114, 0xf, 0xf, false));  // row_shr:4
+      m = max(m, __builtin_amdgcn_update_dpp(0, m, 0x118, 0xf, 0xf, false));  // row_shr:8
+      const int32_t mw = max(max(__builtin_amdgcn_readlane(m, 15), __builtin_amdgcn_readlane(m, 31)),
+                             max(__builtin_amdgcn_readlane(m, 47), __builtin_amdgcn_readlane(m, 63)));
+      const int32_t et = 25 - max(mw >> 10, 1);  // < vexp: some lane was over
+      const float f = __builtin_amdgcn_ldexpf(1.0f, et - vexp);
+#pragma unroll
+      for (int np = 0; np < NP; ++np)
+#pragma unroll
+        for (int m2 = 0; m2 < D / 16; ++m2) oacc[np][m2] *= f;
+      vexp = et;
+    }
+    // 2^vexp as at most two normal f16 factors (-6 <= vexp <= 30), as bits
+    const uint32_t b1 = (uint32_t)(min(vexp, 15) + 15) << 10;
+    const uint32_t b2 = (uint32_t)(max(vexp - 15, 0) + 15) << 10;
+    const v2h f1 = __builtin_bit_cast(v2h, b1 | (b1 << 16));
+    const v2h f2 = __builtin_bit_cast(v2h, b2 | (b2 << 16));
+    lds_u8 *dst = NW == 1 ? const_cast<lds_u8 *>(st) + S::kVS : vsc;
+#pragma unroll
+    for (int i = 0; i < kVW; ++i) {
+      v2h h = __builtin_bit_cast(v2h, v.w[i]) * f1;
+      if (vexp > 15) h *= f2;
+      *reinterpret_cast<__attribute__((address_space(3))) uint32_t *>(dst + 4 * kVW * lane + 4 * i) =
+          __builtin_bit_cast(uint32_t, h);
+    }
+    return dst;
+  }
+  __device__ __forceinline__ const lds_u8 *scale_v(const lds_u8 *st) {
+    VProbe v;
+    const bool over = probe_v(st, v);
+    return apply_v(st, over, v);
+  }
+
+  // Divides the accumulators by 2^vexp (after the last tile).
+  __device__ __forceinline__ void finish() {
+    const float f = __builtin_amdgcn_ldexpf(1.0f, -vexp);
+#pragma unroll
+    for (int np = 0; np < NP; ++np)
+#pragma unroll
+      for (int m = 0; m < D / 16; ++m) oacc[np][m] *= f;
+  }
 
   // Copy tile `tile` (32 tokens) of this work unit HBM -> LDS stage `dst`.
   // Page ids come from `pidv` (lane i holds the partition's i-th page id).
@@ -501,6 +590,17 @@ struct Decoder {
     float sacc[kQR][2][4];
     // tiles wholly below every live row's limit skip the per-token mask
     const bool full = t0 + kTile <= rlim_min;
+    // the V scales' exponent (scale_v), probed before the QK so that it
+    // hides the probe's latency: one wave.  The verify's two waves hold too
+    // many registers across the QK for that and scale after the softmax;
+    // the prefill's (kF16V) waves scale in step(), before its barrier.
+    constexpr bool kEarlyProbe = NW == 1;
+    VProbe vp;
+    bool vover = false;
+    if constexpr (kEarlyProbe) {
+      if (t0 + kTile > len) mask_tail_scales(st, t0);
+      vover = probe_v(st, vp);
+    }
 #pragma unroll
     for (int nt = 0; nt < kQR; ++nt)
 #pragma unroll
@@ -602,6 +702,9 @@ struct Decoder {
       }
     }
 
+    const lds_u8 *vs = vsc;
+    if constexpr (kEarlyProbe) vs = apply_v(st, vover, vp);
+
     // ---- online softmax (base 2, lazily rescaled reference max) ----
     uint32_t pp[NP][4];  // p of the lane's 8 tokens as packed f16 pairs
     uint32_t pl[NP][4];  // kSplitP: p - f16(p), rounded to f16
@@ -690,8 +793,11 @@ struct Decoder {
     // error, exact from an f16 fma, plus (p - f16(p)) * d_v -- and a second
     // MFMA on the same V operand adds it, so the weights are exact to about
     // 2^-22. ----
-    if (t0 + kTile > len) mask_tail_scales(st, t0);
-    pv(st, pp, pl, pz);
+    if constexpr (!kEarlyProbe && !kF16V) {
+      if (t0 + kTile > len) mask_tail_scales(st, t0);
+      vs = scale_v(st);
+    }
+    pv(st, vs, pp, pl, pz);
   }
 
   // kDSplit: tile `tile` (stage `st`) on this wave's half of the dims.
@@ -716,6 +822,11 @@ struct Decoder {
     const int32_t t0 = tok0 + tile * kTile;
     const bool full = t0 + kTile <= rlim_min;
     constexpr int w = W, o = 1 - W;
+    // the PV's V scales (scale_v): probed before the QK, which hides the
+    // probe's latency, and scaled into vsc after it
+    if (t0 + kTile > len) mask_tail_scales(st, t0);
+    VProbe vp;
+    const bool vover = probe_v(st, vp);
     float sacc[2][2][4];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
@@ -746,6 +857,8 @@ struct Decoder {
         }
       }
     }
+
+    const lds_u8 *vs = apply_v(st, vover, vp);
 
     // ---- 2. partial-score exchange ----
     __attribute__((address_space(3))) v4f *ps = reinterpret_cast<__attribute__((address_space(3))) v4f *>(xs);
@@ -837,11 +950,10 @@ struct Decoder {
     }
 
     // ---- 5. PV of all 32 rows over the half's dims ----
-    if (t0 + kTile > len) mask_tail_scales(st, t0);
 #pragma unroll
     for (int bl = 0; bl < kHB; ++bl) {
       const int blk = w * kHB + bl;
-      const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
+      const v4i sv = lds_load<v4i>(vs + 2 * (blk * 32 + 8 * lg));
       v8h pb[2], pbl[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -902,14 +1014,14 @@ struct Decoder {
     }
   }
 
-  // PV of one tile (see compute).
-  __device__ __forceinline__ void pv(const lds_u8 *st, const uint32_t (&pp)[NP][4],
+  // PV of one tile (see compute), with the V scales `vs` (scale_v).
+  __device__ __forceinline__ void pv(const lds_u8 *st, const lds_u8 *vs, const uint32_t (&pp)[NP][4],
                                      const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4]) {
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
       // (ext-vector loads only: an LDS load of the uint4 struct type makes the
       // compiler drain every in-flight copy before it)
-      const v4i sv = lds_load<v4i>(st + S::kVS + 2 * (blk * 32 + 8 * lg));
+      const v4i sv = lds_load<v4i>(vs + 2 * (blk * 32 + 8 * lg));
       uint32_t sc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) sc[i] = (uint32_t)sv[i];
@@ -1039,8 +1151,15 @@ struct Decoder {
     wait_tiles_ahead(ahead);
     if (NW > 1) wg_barrier();  // every wave's copies of tile t have landed
     if constexpr (kF16V) {
+      // the V scales are probed first, so that the widening overlaps the
+      // probe's read; the scaled copy goes to this wave's vsc
+      const int32_t t0 = tok0 + t * kTile;
+      if (t0 + kTile > len) mask_tail_scales(cur, t0);
+      VProbe vp;
+      const bool over = probe_v(cur, vp);
       widen_v(cur);
       if constexpr (kF16K) widen_k(cur);
+      apply_v(cur, over, vp);
       wg_barrier_lds();  // vf16 (and kF16K: kf16) hold tile t
     }
     if constexpr (kDSplit) compute_split(t, cur);
@@ -1491,6 +1610,8 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
   // kDSplit: partial scores [2][64][8] f32, then rescale factors [2][64] f32
   __shared__ __attribute__((aligned(16))) uint8_t xsbuf[Dec::kDSplit ? 2 * 64 * 32 + 2 * 64 * 4 : 16];
+  // NW > 1: each wave's scaled V scales of the tile (Decoder::scale_v)
+  __shared__ __attribute__((aligned(16))) uint8_t vscbuf[NW > 1 ? NW * 2 * D : 16];
 
   Dec dc(p);
   dc.xs = (lds_u8 *)xsbuf;
@@ -1652,7 +1773,9 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   // rows of draft j attend len - q_len + j + 1 positions; row 0 is live
   dc.rlim_min = len - p.q_len + 1;
 
+  dc.vsc = (lds_u8 *)vscbuf + (NW > 1 ? dc.wave * 2 * D : 0);
   dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
+  dc.finish();
 
   if constexpr (Dec::kDSplit) {
     // o of all 32 rows over this wave's half of the dims; (m, l) of its own

@@ -35,6 +35,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   __shared__ int32_t page_list[kPrefillMaxPages];
   __shared__ __attribute__((aligned(16))) uint8_t v_f16[D * 64];  // the tile's V as f16
   __shared__ __attribute__((aligned(16))) uint8_t k_f16[kQF16 ? D * 64 : 16];  // kQF16: the tile's K as f16
+  __shared__ __attribute__((aligned(16))) uint8_t v_scl[kPrefillWaves * 2 * D];  // each wave's scaled V scales
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
 
@@ -115,6 +116,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.pg_lds = (const __attribute__((address_space(3))) int32_t *)page_list;
   dc.vf16 = (lds_u8 *)v_f16;
   dc.kf16 = (lds_u8 *)k_f16;
+  dc.vsc = (lds_u8 *)v_scl + dc.wave * 2 * D;
 
   const int32_t G = p.q_heads / g.kv_heads;  // rows of one chunk token
   // row r of the block: chunk token j0 + r / G, q head kvh*G + r % G; the
@@ -143,6 +145,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
 
   dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
+  dc.finish();
 
   float l = dc.lrun[0];
   l += __shfl_xor(l, 16);

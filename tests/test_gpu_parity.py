@@ -41,7 +41,7 @@ class Scene:
     """A shuffled page pool holding B sequences of the given lengths."""
 
     def __init__(self, rkv, rko, Hkv, D, PT, lens, seed=0, slack=1.1, outliers=0.0,
-                 src_bf16=False, rule=0, extra_rows=None):
+                 src_bf16=False, rule=0, extra_rows=None, v_mul=None):
         torch = _torch()
         rng = np.random.default_rng(seed)
         self.Hkv, self.D, self.PT = Hkv, D, PT
@@ -67,6 +67,11 @@ class Scene:
                 ch = rng.choice(D, nch, replace=False)
                 k[:, h, ch] *= 8
                 v[:, h, ch] *= 8
+        if v_mul is not None:
+            # V magnitude: a factor, or a function of each row's position
+            pos = np.concatenate([np.arange(L) for L in lens]) if n else np.zeros(0, np.int64)
+            m = v_mul(pos) if callable(v_mul) else np.full(n, v_mul)
+            v *= np.asarray(m, np.float32)[:, None, None]
         if src_bf16:
             k = rko.bf16_to_f32(rko.f32_to_bf16(k)).reshape(k.shape)
             v = rko.bf16_to_f32(rko.f32_to_bf16(v)).reshape(v.shape)
