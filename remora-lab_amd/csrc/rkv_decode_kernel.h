@@ -295,6 +295,11 @@ struct Decoder {
   // [n-tile][own block] and oacc[0] holds [n-tile][own 16-dim tile].  Not on
   // 16-token pages: their copy plan leaves the split too few registers.
   static constexpr bool kDSplit = NW == 2 && kF16K && !kF16V && NS == 2 && !kSmall;
+  // kPipe (the prefill with a bf16 query: kF16V and kF16K): the workgroup
+  // widens tile t+1 into a second f16 buffer while it computes tile t (see
+  // run_pipe), so the tile's compute reads only f16 buffers and the stage
+  // is refilled as soon as it is widened: one barrier per tile.
+  static constexpr bool kPipe = kF16V && kF16K;
   static constexpr int kHB = NB / 2;  // kDSplit: blocks of a wave's half
   static constexpr int kHM = D / 32;  // kDSplit: 16-dim PV tiles of a wave's half
 
@@ -316,6 +321,7 @@ struct Decoder {
   QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
   v8h qf[kQF];             // kF16K: query f16 operand per Q8 block (see load_q_f16)
   lds_u8 *kf16;            // kF16K: [token][D] f16, 16-byte chunk c of row r at c ^ (r & (D/8 - 1))
+  const lds_u8 *ks;        // kPipe: the computed tile's K scales (copied out of its stage)
   lds_u8 *xs;              // kDSplit: partial scores [wave][lane][8] f32, then alphas [wave][lane] f32
   float rmul[NP];
   int32_t rlim[NP];
@@ -611,7 +617,7 @@ struct Decoder {
 #pragma unroll
       for (int blk = 0; blk < NB; ++blk) {
         // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
-        const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
+        const v8h dk8 = lds_load<v8h>((kPipe ? ks : st + S::kKS) + 2 * (blk * 32 + 8 * lg));
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const int krow = 16 * mt + li;
@@ -1102,9 +1108,16 @@ struct Decoder {
   // Chunk (dim d, k-group g) is the 8 tokens lane (d, g) of the PV MFMA
   // holds: 4g..4g+3 then 16+4g..16+4g+3 (the halves are swapped in the
   // stage when (d >> 2) & 1, as the tile copy put them).
-  __device__ __forceinline__ void widen_v(const lds_u8 *st) {
+  __device__ __forceinline__ void widen_v(const lds_u8 *st, lds_u8 *dst) {
     constexpr int kChunks = 4 * D;
-    for (int c = wave * 64 + lane; c < kChunks; c += 64 * NW) {
+    // a fixed trip count (chunks c = wave*64 + lane + i*64*NW) keeps the
+    // widening straight-line code that the compiler can interleave with the
+    // compute that follows it
+    constexpr int kIt = (kChunks + 64 * NW - 1) / (64 * NW);
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+      const int c = (i * NW + wave) * 64 + lane;
+      if (kChunks % (64 * NW) != 0 && c >= kChunks) continue;
       const int d = c >> 2, g = c & 3;
       const int sw = (d >> 2) & 1;
       const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * g);
@@ -1113,29 +1126,97 @@ struct Decoder {
       v8x4_to_f16(w0, a0, a1);
       v8x4_to_f16(w1, a2, a3);
       const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-      *reinterpret_cast<__attribute__((address_space(3))) v8h *>(vf16 + 16 * (4 * d + (g ^ (d & 3)))) = va;
+      *reinterpret_cast<__attribute__((address_space(3))) v8h *>(dst + 16 * (4 * d + (g ^ (d & 3)))) = va;
     }
   }
+
 
   // kF16K: widen this wave's share of the landed tile's K codes into kf16.
   // Physical 16-byte chunk pc of K row r holds logical chunk pc ^ (r mod
   // D/16), the codes of dims 16*lc .. +15 (signed; xor 0x80 makes them the
   // biased form v8x4_to_f16 takes).  They become f16 chunks 2*lc and 2*lc+1.
-  __device__ __forceinline__ void widen_k(const lds_u8 *st) {
+  __device__ __forceinline__ void widen_k(const lds_u8 *st, lds_u8 *dst) {
     constexpr int kCPR = D / 16;
-    for (int c = wave * 64 + lane; c < 32 * kCPR; c += 64 * NW) {
+    constexpr int kChunks = 32 * kCPR;
+    constexpr int kIt = (kChunks + 64 * NW - 1) / (64 * NW);  // fixed trip count, as widen_v
+#pragma unroll
+    for (int i = 0; i < kIt; ++i) {
+      const int c = (i * NW + wave) * 64 + lane;
+      if (kChunks % (64 * NW) != 0 && c >= kChunks) continue;
       const int r = c / kCPR, pc = c % kCPR;
       const int lc = pc ^ (r & (kCPR - 1));
       const v4i w = lds_load<v4i>(st + S::kKC + r * D + 16 * pc);
       v2h h[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v8x4_to_f16((uint32_t)w[i] ^ 0x80808080u, h[2 * i], h[2 * i + 1]);
+      for (int j = 0; j < 4; ++j) v8x4_to_f16((uint32_t)w[j] ^ 0x80808080u, h[2 * j], h[2 * j + 1]);
       const v8h f0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
       const v8h f1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
-      lds_u8 *row = kf16 + r * (2 * D);
+      lds_u8 *row = dst + r * (2 * D);
       *reinterpret_cast<__attribute__((address_space(3))) v8h *>(row + 16 * ((2 * lc) ^ (r & (D / 8 - 1)))) = f0;
       *reinterpret_cast<__attribute__((address_space(3))) v8h *>(row + 16 * ((2 * lc + 1) ^ (r & (D / 8 - 1)))) = f1;
     }
+  }
+
+
+  // kPipe: an f16 buffer holds one tile as the compute reads it: K widened
+  // [token][D] (kf16's layout, 64*D bytes), V widened (vf16's layout, 64*D
+  // bytes), then the tile's K scales as staged (2*D bytes).
+  static constexpr int kFK = 0, kFV = 64 * D, kFS = 128 * D;
+  static constexpr int kFBytes = 130 * D;
+
+  // kPipe: tile t's stage `src` into f16 buffer `f`, this wave's share.
+  __device__ __forceinline__ void widen_into(const lds_u8 *src, lds_u8 *f) {
+    widen_v(src, f + kFV);
+    widen_k(src, f + kFK);
+    for (int c = wave * 64 + lane; c < D / 8; c += 64 * NW)
+      *reinterpret_cast<__attribute__((address_space(3))) v4i *>(f + kFS + 16 * c) =
+          lds_load<v4i>(src + S::kKS + 16 * c);
+  }
+  // kPipe: tile t's V scales from its stage `src` into this wave's vsc (the
+  // tail tile's junk scales zeroed first), with the accumulators' 2^vexp
+  // step (scale_v); after tile t-1's PV, which used the previous vsc.
+  __device__ __forceinline__ void prep_v(int t, const lds_u8 *src) {
+    const int32_t t0 = tok0 + t * kTile;
+    if (t0 + kTile > len) mask_tail_scales(src, t0);
+    scale_v(src);
+  }
+  // kPipe, step t.  Entering it, f16 buffer fc holds tile t (written by every
+  // wave in step t-1), this wave's vsc holds tile t's V scales, and tile
+  // t+1's copies into stage rn were issued in step t-1.  One barrier: after
+  // it tile t+1 has landed, fc is complete, and every wave is done with the
+  // stage rc (widened in step t-1) and with fn (computed in step t-1).  Then
+  // tile t+2's copies go into rc, tile t+1 is widened into fn while tile t
+  // is computed from fc, and tile t+1's V scales are taken after tile t's PV.
+  __device__ __forceinline__ void pipe_step(int t, lds_u8 *__restrict__ rc, lds_u8 *__restrict__ rn,
+                                            lds_u8 *__restrict__ fc, lds_u8 *__restrict__ fn) {
+    const bool more = t + 1 < n_tiles;
+    if (more) __builtin_amdgcn_s_waitcnt(kWaitBase);  // this wave's copies of tile t+1
+    wg_barrier_lds();
+    if (t + 2 < n_tiles) issue(t + 2, rc);
+    if (more) widen_into(rn, fn);
+    kf16 = fc + kFK;
+    vf16 = fc + kFV;
+    ks = fc + kFS;
+    compute(t, rc);  // reads fc and vsc only: rc is being refilled
+    if (more) prep_v(t + 1, rn);
+  }
+  // kPipe: the tile loop over stages r0, r1 and f16 buffers f0, f1 (tile k
+  // in r[k % 2] and f[k % 2]).
+  __device__ __forceinline__ void run_pipe(lds_u8 *__restrict__ r0, lds_u8 *__restrict__ r1,
+                                           lds_u8 *__restrict__ f0, lds_u8 *__restrict__ f1) {
+    if (n_tiles == 0) return;
+    issue(0, r0);
+    if (n_tiles > 1) issue(1, r1);
+    wait_tiles_ahead(n_tiles > 1 ? 1 : 0);
+    wg_barrier();  // every wave's copies of tile 0 have landed
+    widen_into(r0, f0);
+    prep_v(0, r0);
+    int t = 0;
+    for (; t + 1 < n_tiles; t += 2) {
+      pipe_step(t, r0, r1, f0, f1);
+      pipe_step(t + 1, r1, r0, f1, f0);
+    }
+    if (t < n_tiles) pipe_step(t, r0, r1, f0, f1);
   }
 
   __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
@@ -1157,8 +1238,8 @@ struct Decoder {
       if (t0 + kTile > len) mask_tail_scales(cur, t0);
       VProbe vp;
       const bool over = probe_v(cur, vp);
-      widen_v(cur);
-      if constexpr (kF16K) widen_k(cur);
+      widen_v(cur, vf16);
+      if constexpr (kF16K) widen_k(cur, kf16);
       apply_v(cur, over, vp);
       wg_barrier_lds();  // vf16 (and kF16K: kf16) hold tile t
     }

@@ -33,8 +33,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   using S = StageShape<D>;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
   __shared__ int32_t page_list[kPrefillMaxPages];
-  __shared__ __attribute__((aligned(16))) uint8_t v_f16[D * 64];  // the tile's V as f16
-  __shared__ __attribute__((aligned(16))) uint8_t k_f16[kQF16 ? D * 64 : 16];  // kQF16: the tile's K as f16
+  // kQF16: two f16 buffers, each a tile's K and V widened and its K scales
+  // (Decoder::run_pipe widens tile t+1 into one while tile t is computed from
+  // the other); otherwise the tile's V as f16
+  __shared__ __attribute__((aligned(16))) uint8_t f16buf[kQF16 ? 2 * Dec::kFBytes : D * 64];
   __shared__ __attribute__((aligned(16))) uint8_t v_scl[kPrefillWaves * 2 * D];  // each wave's scaled V scales
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
@@ -98,7 +100,9 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
 
   Dec dc(p);
   dc.lane = threadIdx.x & 63;
-  dc.wave = (int)(threadIdx.x >> 6);
+  // uniform within a wave: a scalar, so that the per-wave choices (which
+  // tile copies it issues, which chunks it widens) are scalar branches
+  dc.wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   dc.li = dc.lane & 15;
   dc.lg = dc.lane >> 4;
   const int lane = dc.lane, li = dc.li, lg = dc.lg;
@@ -114,8 +118,8 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.pg_first = pg0;
   dc.pidv = 0;
   dc.pg_lds = (const __attribute__((address_space(3))) int32_t *)page_list;
-  dc.vf16 = (lds_u8 *)v_f16;
-  dc.kf16 = (lds_u8 *)k_f16;
+  dc.vf16 = (lds_u8 *)f16buf;
+  dc.kf16 = (lds_u8 *)f16buf;
   dc.vsc = (lds_u8 *)v_scl + dc.wave * 2 * D;
 
   const int32_t G = p.q_heads / g.kv_heads;  // rows of one chunk token
@@ -144,7 +148,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
 
-  dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
+  if constexpr (kQF16) {
+    static_assert(NS == 2, "the pipelined prefill runs a two-stage ring");
+    dc.run_pipe((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)f16buf, (lds_u8 *)f16buf + Dec::kFBytes);
+  } else {
+    dc.run((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)lds[NS - 1]);
+  }
   dc.finish();
 
   float l = dc.lrun[0];
