@@ -104,15 +104,20 @@ __device__ __forceinline__ v4f f16x4_to_f32(uint2 w) {
 // 16-token pages hold half a tile each: the code runs are still 16-byte
 // copies, but the lane-ordered scale runs interleave the two pages every 4
 // bytes, so they use 4-byte copies.
-template <int D, bool kSmallPage, bool kKReg = false>
+template <int D, bool kSmallPage, bool kKReg = false, int NW = 1>
 struct ChunkPlan {
   using S = StageShape<D, kKReg>;
   static constexpr int kNKC = D / 32;                       // 1 KiB K-code (or V-code) copies
   static constexpr int kN16 = kSmallPage ? 2 * kNKC : S::kInstr;
   static constexpr int kN4 = kSmallPage ? 2 * (D / 128) : 0;  // 256-byte scale copies
   static constexpr int kInstr = kN16 + kN4;                  // vmcnt units per tile
-  uint32_t off[kN16 + kN4];
-  uint32_t mul[kN16 + kN4];  // D for code runs, D/16 for scale runs (pages >= 32 tokens)
+  // Pages of >= 32 tokens with NW waves: wave w issues copies k = i*NW + w
+  // and holds only their offsets (entry i), so its copies go out as
+  // straight-line code; 16-token pages keep every copy's entry.
+  static constexpr int kWaves = kSmallPage ? 1 : NW;
+  static constexpr int kPer = (kN16 + kWaves - 1) / kWaves;  // 16-byte copy entries per wave
+  uint32_t off[kPer + kN4];
+  uint32_t mul[kPer + kN4];  // D for code runs, D/16 for scale runs (pages >= 32 tokens)
   uint32_t halves;           // bit k: chunk k lies in the tile's second 16-token half
   __host__ __device__ static constexpr int dst16(int k) {  // LDS byte offset of 16-B copy k
     return kSmallPage ? (k < kNKC ? S::kKC + 1024 * k : S::kVC + 1024 * (k - kNKC)) : 1024 * k;
@@ -122,11 +127,11 @@ struct ChunkPlan {
   }
 };
 
-template <int D, bool kSmallPage, bool kKReg = false>
-__device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage, kKReg> &pl, const Geo &g,
-                                          int lane) {
+template <int D, bool kSmallPage, bool kKReg = false, int NW = 1>
+__device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage, kKReg, NW> &pl, const Geo &g,
+                                          int lane, int wave = 0) {
   using S = StageShape<D, kKReg>;
-  using PL = ChunkPlan<D, kSmallPage, kKReg>;
+  using PL = ChunkPlan<D, kSmallPage, kKReg, NW>;
   const uint32_t RB = (uint32_t)region_bytes(g);
   const uint32_t PTD = (uint32_t)g.page_tokens * D;
   pl.halves = 0;
@@ -154,7 +159,8 @@ __device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage, kKReg> &pl, c
     }
   } else if constexpr (!kSmallPage) {
 #pragma unroll
-    for (int k = 0; k < S::kInstr; ++k) {
+    for (int i = 0; i < PL::kPer; ++i) {
+      const int k = i * PL::kWaves + wave;  // copy k (past the last: unused)
       const int c = 64 * k + lane;
       uint32_t off = 0, is_scale = 0;
       if (c < 2 * D) {  // K codes: row r, physical chunk pc holds logical chunk pc ^ (r mod CPR)
@@ -175,8 +181,8 @@ __device__ __forceinline__ void make_plan(ChunkPlan<D, kSmallPage, kKReg> &pl, c
         off = RB + PTD + 2u * (uint32_t)(32 * (i >> 2) + 8 * (i & 3));
         is_scale = 1;
       }  // else: padding lane of the last copy, re-reads chunk 0 of the tile
-      pl.off[k] = off;
-      pl.mul[k] = is_scale ? (uint32_t)(D / 16) : (uint32_t)D;
+      pl.off[i] = off;
+      pl.mul[i] = is_scale ? (uint32_t)(D / 16) : (uint32_t)D;
     }
   } else {
 #pragma unroll
@@ -305,6 +311,7 @@ struct Decoder {
 
   const DecodeLaunch &p;
   int lane, li, lg, kvh, b, wave;
+  int swave;               // wave, read into a scalar: indexes this wave's tile copies
   int32_t seq, len, tok0, tok_end, n_tiles;
   int32_t app_mode;        // 0: no rows to append here; 1: before the first copy; 2: after the prologue copies
   int32_t app_first;       // first tile of this partition that holds an appended row
@@ -316,7 +323,7 @@ struct Decoder {
   lds_u8 *vf16;            // kF16V: [dim][4 k-groups] x 8 f16, k-group slot lg ^ (dim & 3)
   const uint8_t *kv_base;  // pages + kv head offset
   uint64_t PB;
-  ChunkPlan<D, kSmall, kKReg> plan;
+  ChunkPlan<D, kSmall, kKReg, NW> plan;
   QOp kreg[2][kQC];        // kKReg: K codes of the tile being computed (A operands)
   QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
   v8h qf[kQF];             // kF16K: query f16 operand per Q8 block (see load_q_f16)
@@ -425,19 +432,21 @@ struct Decoder {
     const Geo &g = p.g;
     const int32_t t0 = tok0 + tile * kTile;
     const int32_t pi = t0 / g.page_tokens - pg_first;
-    using PL = ChunkPlan<D, kSmall, kKReg>;
+    using PL = ChunkPlan<D, kSmall, kKReg, NW>;
     if constexpr (!kSmall) {
       const int32_t pid = kPageList ? __builtin_amdgcn_readfirstlane(pg_lds[pi])
                                     : __builtin_amdgcn_readlane(pidv, pi);
       const uint8_t *base = kv_base + (uint64_t)pid * PB;
       const uint32_t s0 = (uint32_t)(t0 % g.page_tokens);
+      // this wave's copies k = i*NW + wave, entry i of its plan
 #pragma unroll
-      for (int k = 0; k < PL::kN16; ++k) {
-        if (NW > 1 && k % NW != wave) continue;
+      for (int i = 0; i < PL::kPer; ++i) {
+        const int k = i * PL::kWaves + swave;
+        if (PL::kWaves > 1 && PL::kN16 % PL::kWaves != 0 && k >= PL::kN16) break;
         // kKReg: copies 0..2D/64-1 are V codes, the rest scales (their
         // padding lanes read inside the region either way)
-        const uint32_t mul = kKReg ? (64 * k < 2 * D ? (uint32_t)D : (uint32_t)(D / 16)) : plan.mul[k];
-        const uint32_t voff = plan.off[k] + s0 * mul;
+        const uint32_t mul = kKReg ? (64 * k < 2 * D ? (uint32_t)D : (uint32_t)(D / 16)) : plan.mul[i];
+        const uint32_t voff = plan.off[i] + s0 * mul;
         __builtin_amdgcn_global_load_lds(base + voff, dst + PL::dst16(k), 16, 0, kCpol);
       }
     } else {
@@ -1090,7 +1099,7 @@ struct Decoder {
   // waves; counting floor(kInstr / NW) per tile is exact for the waves with
   // that many and waits one copy longer for the others.
   __device__ __forceinline__ static void wait_tiles_ahead(int ahead) {
-    constexpr int kI = ChunkPlan<D, kSmall, kKReg>::kInstr / NW;
+    constexpr int kI = ChunkPlan<D, kSmall, kKReg, NW>::kInstr / NW;
     static_assert(kI >= 1, "every wave issues at least one copy per tile");
     if (ahead >= 2) {
       constexpr int n = 2 * kI;
@@ -1698,6 +1707,11 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   dc.xs = (lds_u8 *)xsbuf;
   dc.lane = threadIdx.x & 63;
   dc.wave = NW > 1 ? (int)(threadIdx.x >> 6) : 0;
+  // the same value read into a scalar, so that the wave's share of each
+  // tile's copies (ChunkPlan) is addressed with scalar arithmetic (the
+  // split verify's per-wave code paths keep the vector form: with a scalar
+  // they hold more registers than the wave has)
+  dc.swave = NW > 1 ? (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) : 0;
   const int r0 = 16 * dc.wave;  // first query row of this wave
   dc.li = dc.lane & 15;  // MFMA row/column within a 16-lane group
   dc.lg = dc.lane >> 4;  // MFMA k-group
@@ -1740,7 +1754,7 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   // ---- prologue loads, issued together so their latencies overlap: the
   // partition's page ids, this entry's appended-row positions and the query
   // rows (each of them needs only the entry and partition located above)
-  make_plan<D, kSmall, kKReg>(dc.plan, g, lane);
+  make_plan<D, kSmall, kKReg, NW>(dc.plan, g, lane, dc.swave);
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
   // The partition's page ids, one per lane (partitions start on a page

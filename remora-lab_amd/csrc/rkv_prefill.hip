@@ -103,6 +103,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   // uniform within a wave: a scalar, so that the per-wave choices (which
   // tile copies it issues, which chunks it widens) are scalar branches
   dc.wave = (int)__builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  dc.swave = dc.wave;
   dc.li = dc.lane & 15;
   dc.lg = dc.lane >> 4;
   const int lane = dc.lane, li = dc.li, lg = dc.lg;
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   }
   // chunk token j0 (row 0 of the block) attends the fewest positions
   dc.rlim_min = jn > 0 ? ctx + j0 + 1 : 0;
-  make_plan<D, kSmall>(dc.plan, g, lane);
+  make_plan<D, kSmall, false, kPrefillWaves>(dc.plan, g, lane, dc.swave);
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
 
