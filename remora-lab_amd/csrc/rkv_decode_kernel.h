@@ -622,29 +622,57 @@ struct Decoder {
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) sacc[nt][mt][r] = 0.0f;
-    if constexpr (kF16K) {
-#pragma unroll
-      for (int blk = 0; blk < NB; ++blk) {
-        // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
-        const v8h dk8 = lds_load<v8h>((kPipe ? ks : st + S::kKS) + 2 * (blk * 32 + 8 * lg));
+    if constexpr (kF16K && kF16V) {
+      // K f16 operands and scales from LDS: block blk+1's are read before
+      // block blk's MFMAs, so each block's LDS latency hides behind the
+      // previous block's work.  Lane-ordered scales: 8 f16 = tokens 4*lg+r
+      // of M-tile 0, then of M-tile 1; the operand of M-tile mt is dims
+      // 32*blk + 8*lg .. +7 of token row 16*mt + li, f16 chunk 4*blk + lg.
+      const lds_u8 *ksrc = kPipe ? ks : st + S::kKS;
+      v8h ka[2], kn[2], dka, dkn;
+      auto load_blk = [&](int blk, v8h(&a)[2], v8h &dk) {
+        dk = lds_load<v8h>(ksrc + 2 * (blk * 32 + 8 * lg));
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) {
           const int krow = 16 * mt + li;
-          v8h a;
-          if constexpr (kF16V) {
-            // dims 32*blk + 8*lg .. +7 = f16 chunk 4*blk + lg of the row
-            const int pc = (4 * blk + lg) ^ (krow & (D / 8 - 1));
-            a = lds_load<v8h>(kf16 + krow * (2 * D) + 16 * pc);
-          } else {
-            // the int8 operand (see the kWide QK below), widened
-            const int pc = (2 * blk + (lg >> 1)) ^ (krow & (S::kCPR - 1));
-            const int64_t k8 = kKReg ? kreg[mt][blk]
-                                     : lds_load<int64_t>(st + S::kKC + krow * D + 16 * pc + 8 * (lg & 1));
-            v2h h0, h1, h2, h3;
-            v8x4_to_f16((uint32_t)k8 ^ 0x80808080u, h0, h1);
-            v8x4_to_f16((uint32_t)((uint64_t)k8 >> 32) ^ 0x80808080u, h2, h3);
-            a = v8h{h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
-          }
+          const int pc = (4 * blk + lg) ^ (krow & (D / 8 - 1));
+          a[mt] = lds_load<v8h>(kf16 + krow * (2 * D) + 16 * pc);
+        }
+      };
+      load_blk(0, ka, dka);
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) {
+        if (blk + 1 < NB) load_blk(blk + 1, kn, dkn);
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const v4f z = {0.f, 0.f, 0.f, 0.f};
+          const v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[mt], qf[blk], z, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            sacc[0][mt][r] = __builtin_fmaf(c[r], (float)dka[4 * mt + r], sacc[0][mt][r]);
+        }
+        if (blk + 1 < NB) {
+          ka[0] = kn[0];
+          ka[1] = kn[1];
+          dka = dkn;
+        }
+      }
+    } else if constexpr (kF16K) {
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) {
+        // lane-ordered scales: 8 f16 = tokens 4*lg+r of M-tile 0, then of M-tile 1
+        const v8h dk8 = lds_load<v8h>(st + S::kKS + 2 * (blk * 32 + 8 * lg));
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+          const int krow = 16 * mt + li;
+          // the int8 operand (see the kWide QK below), widened
+          const int pc = (2 * blk + (lg >> 1)) ^ (krow & (S::kCPR - 1));
+          const int64_t k8 = kKReg ? kreg[mt][blk]
+                                   : lds_load<int64_t>(st + S::kKC + krow * D + 16 * pc + 8 * (lg & 1));
+          v2h h0, h1, h2, h3;
+          v8x4_to_f16((uint32_t)k8 ^ 0x80808080u, h0, h1);
+          v8x4_to_f16((uint32_t)((uint64_t)k8 >> 32) ^ 0x80808080u, h2, h3);
+          const v8h a = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
           const v4f z = {0.f, 0.f, 0.f, 0.f};
           const v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[blk], z, 0, 0, 0);
 #pragma unroll
@@ -1029,70 +1057,106 @@ struct Decoder {
     }
   }
 
+  // The PV weights of one Q8 block from its lane-ordered V scales `sv`:
+  // pb = p * d_v and (kSplitP) pbl = its second term (see compute).
+  __device__ __forceinline__ void pv_weights(const v4i sv, const uint32_t (&pp)[NP][4],
+                                             const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4],
+                                             v8h (&pb)[NP], v8h (&pbl)[NP]) const {
+#pragma unroll
+    for (int np = 0; np < NP; ++np) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const v2h ph = __builtin_bit_cast(v2h, pp[np][i]);
+        const v2h dv = __builtin_bit_cast(v2h, (uint32_t)sv[i]);
+        v2h hi;
+        if constexpr (kColSplit) {
+          // lanes li < 8: q = 0, so e = f16(p)*d_v rounded once and the
+          // second fma adds 0 * d_v; lanes li >= 8: e is the product's
+          // exact rounding error and the result the second weight term
+          const v2h q = __builtin_bit_cast(v2h, pz[np][i]) * dv;
+          const v2h e = __builtin_elementwise_fma(ph, dv, -q);
+          hi = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, e);
+        } else {
+          const v2h prod = ph * dv;
+          hi = prod;
+          if constexpr (kSplitP) {
+            const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
+            const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, err);
+            pbl[np][2 * i] = lo[0];
+            pbl[np][2 * i + 1] = lo[1];
+          }
+        }
+        pb[np][2 * i] = hi[0];
+        pb[np][2 * i + 1] = hi[1];
+      }
+    }
+  }
+  // The PV MFMAs of 16-dim tile m of every n-tile on V operand va.
+  __device__ __forceinline__ void pv_mfma(int m, const v8h va, const v8h (&pb)[NP], const v8h (&pbl)[NP]) {
+#pragma unroll
+    for (int np = 0; np < NP; ++np) {
+      oacc[np][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[np], oacc[np][m], 0, 0, 0);
+      if constexpr (kSplitP && !kColSplit)
+        oacc[np][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[np], oacc[np][m], 0, 0, 0);
+    }
+  }
+
   // PV of one tile (see compute), with the V scales `vs` (scale_v).
   __device__ __forceinline__ void pv(const lds_u8 *st, const lds_u8 *vs, const uint32_t (&pp)[NP][4],
                                      const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4]) {
+    if constexpr (kF16V) {
+      // V f16 operands and scales from LDS: block blk+1's are read before
+      // block blk's weights and MFMAs, so each block's LDS latency hides
+      // behind the previous block's work.  The operand of dim tile hm is
+      // the 8 tokens lane (d = 32*blk + 16*hm + li, lg) takes.
+      v4i svc, svn;
+      v8h vac[2], van[2];
+      auto load_blk = [&](int blk, v4i &sv, v8h(&va)[2]) {
+        sv = lds_load<v4i>(vs + 2 * (blk * 32 + 8 * lg));
+#pragma unroll
+        for (int hm = 0; hm < 2; ++hm) {
+          const int d = 32 * blk + 16 * hm + li;
+          va[hm] = lds_load<v8h>(vf16 + 16 * (4 * d + (lg ^ (d & 3))));
+        }
+      };
+      load_blk(0, svc, vac);
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk) {
+        if (blk + 1 < NB) load_blk(blk + 1, svn, van);
+        v8h pb[NP], pbl[NP];
+        pv_weights(svc, pp, pl, pz, pb, pbl);
+#pragma unroll
+        for (int hm = 0; hm < 2; ++hm) pv_mfma(2 * blk + hm, vac[hm], pb, pbl);
+        if (blk + 1 < NB) {
+          svc = svn;
+          vac[0] = van[0];
+          vac[1] = van[1];
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int blk = 0; blk < NB; ++blk) {
       // (ext-vector loads only: an LDS load of the uint4 struct type makes the
       // compiler drain every in-flight copy before it)
       const v4i sv = lds_load<v4i>(vs + 2 * (blk * 32 + 8 * lg));
-      uint32_t sc[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) sc[i] = (uint32_t)sv[i];
       v8h pb[NP], pbl[NP];
-#pragma unroll
-      for (int np = 0; np < NP; ++np) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const v2h ph = __builtin_bit_cast(v2h, pp[np][i]);
-          const v2h dv = __builtin_bit_cast(v2h, sc[i]);
-          v2h hi;
-          if constexpr (kColSplit) {
-            // lanes li < 8: q = 0, so e = f16(p)*d_v rounded once and the
-            // second fma adds 0 * d_v; lanes li >= 8: e is the product's
-            // exact rounding error and the result the second weight term
-            const v2h q = __builtin_bit_cast(v2h, pz[np][i]) * dv;
-            const v2h e = __builtin_elementwise_fma(ph, dv, -q);
-            hi = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, e);
-          } else {
-            const v2h prod = ph * dv;
-            hi = prod;
-            if constexpr (kSplitP) {
-              const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
-              const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, err);
-              pbl[np][2 * i] = lo[0];
-              pbl[np][2 * i + 1] = lo[1];
-            }
-          }
-          pb[np][2 * i] = hi[0];
-          pb[np][2 * i + 1] = hi[1];
-        }
-      }
+      pv_weights(sv, pp, pl, pz, pb, pbl);
 #pragma unroll
       for (int hm = 0; hm < 2; ++hm) {
         const int d = 32 * blk + 16 * hm + li;
         const int sw = (d >> 2) & 1;
-        v8h va;
-        if constexpr (kF16V) {
-          va = lds_load<v8h>(vf16 + 16 * (4 * d + (lg ^ (d & 3))));
-        } else {
-          const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * lg);
-          const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * lg);
-          v2h a0, a1, a2, a3;
-          v8x4_to_f16(w0, a0, a1);
-          v8x4_to_f16(w1, a2, a3);
-          va = v8h{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-        }
-#pragma unroll
-        for (int np = 0; np < NP; ++np) {
-          oacc[np][2 * blk + hm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[np], oacc[np][2 * blk + hm], 0, 0, 0);
-          if constexpr (kSplitP && !kColSplit)
-            oacc[np][2 * blk + hm] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[np], oacc[np][2 * blk + hm], 0, 0, 0);
-        }
+        const uint32_t w0 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * sw + 4 * lg);
+        const uint32_t w1 = lds_load<uint32_t>(st + S::kVC + d * 32 + 16 * (sw ^ 1) + 4 * lg);
+        v2h a0, a1, a2, a3;
+        v8x4_to_f16(w0, a0, a1);
+        v8x4_to_f16(w1, a2, a3);
+        const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        pv_mfma(2 * blk + hm, va, pb, pbl);
       }
     }
   }
+
 
   // vmcnt wait for the tile about to be computed when `ahead` later tiles'
   // copies are still in flight.  A tile is kInstr copies, split over the NW
