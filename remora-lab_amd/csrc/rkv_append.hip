@@ -76,21 +76,30 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
     seq = a.seq_ids[row0 + tid];
     pos = a.positions[row0 + tid];
   }
-  constexpr int kTasks = kAppRows * 2 * NB * 4;
+  // kWhole (32-row workgroups): one lane per (row, kind, block) task, its 32
+  // values in registers (q8_quantize_block: no shuffles, one scale per
+  // lane); 8-row workgroups keep 4 lanes per block so that every thread has
+  // a task.  Tasks run block fastest, so consecutive lanes read consecutive
+  // source bytes.
+  constexpr bool kWhole = kAppRows == 32;
+  constexpr int kVPL = kWhole ? 32 : 8;  // values per lane and task
+  constexpr int kTasks = kAppRows * 2 * NB * (32 / kVPL);
   constexpr int kPer = kTasks / 256;
-  static_assert(kTasks % 256 == 0, "every thread takes part in every shuffle round");
-  float v[kPer][8];
+  static_assert(kTasks % 256 == 0, "every thread takes part in every task round");
+  float v[kPer][kVPL];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int t = 256 * i + tid;
-    const int sub = t & 3;
-    const int blk = (t >> 2) % NB;
-    const int kind = ((t >> 2) / NB) & 1;
-    const int r = min((t >> 2) / NB / 2, nr - 1);
-    load_src8<kBf16>(kind == 0 ? a.k_src : a.v_src,
-                     ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
-                         (uint64_t)(blk * 32 + sub * 8),
-                     v[i]);
+    const int sub = kWhole ? 0 : t & 3;
+    const int tb = kWhole ? t : t >> 2;
+    const int blk = tb % NB;
+    const int kind = (tb / NB) & 1;
+    const int r = min(tb / NB / 2, nr - 1);
+    const uint64_t off = ((uint64_t)(row0 + r) * (uint64_t)g.kv_heads + (uint64_t)kvh) * D +
+                         (uint64_t)(blk * 32 + sub * 8);
+#pragma unroll
+    for (int e = 0; e < kVPL / 8; ++e)
+      load_src8<kBf16>(kind == 0 ? a.k_src : a.v_src, off + 8 * e, &v[i][8 * e]);
   }
 
   // ---- rows' destinations (wave 0) --------------------------------------
@@ -131,14 +140,25 @@ __global__ __launch_bounds__(256) void append_kernel(AppendLaunch a) {
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int t = 256 * i + tid;
-    const int sub = t & 3;
-    const int blk = (t >> 2) % NB;
-    const int kind = ((t >> 2) / NB) & 1;
-    const int r = (t >> 2) / NB / 2;
+    const int sub = kWhole ? 0 : t & 3;
+    const int tb = kWhole ? t : t >> 2;
+    const int blk = tb % NB;
+    const int kind = (tb / NB) & 1;
+    const int r = tb / NB / 2;
     uint16_t scale;
-    uint64_t c = q8_quantize_values<8>(v[i], kRule, scale);
-    if (kind == 1) c ^= 0x8080808080808080ull;  // V codes are stored biased (code_bias)
-    *reinterpret_cast<uint64_t *>(&codes[kind][r][blk * 32 + sub * 8]) = c;
+    if constexpr (kWhole) {
+      uint32_t c[8];
+      q8_quantize_block(v[i], kRule, scale, c);
+      const uint32_t bias = kind == 1 ? 0x80808080u : 0u;  // V codes are stored biased (code_bias)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<uint2 *>(&codes[kind][r][blk * 32 + 8 * j]) =
+            uint2{c[2 * j] ^ bias, c[2 * j + 1] ^ bias};
+    } else {
+      uint64_t c = q8_quantize_values<8>(v[i], kRule, scale);
+      if (kind == 1) c ^= 0x8080808080808080ull;  // V codes are stored biased (code_bias)
+      *reinterpret_cast<uint64_t *>(&codes[kind][r][blk * 32 + sub * 8]) = c;
+    }
     if (sub == 0) scl[kind][r][blk] = scale;
   }
   __syncthreads();

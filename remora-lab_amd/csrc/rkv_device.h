@@ -155,11 +155,20 @@ __device__ inline uint16_t f32_to_bf16_rtne(float v) {
   return (uint16_t)(u >> 16);
 }
 
-// Rust `roundf(x) as i32` then clamp to [-127, 127] (NaN -> 0).
-__device__ inline int32_t q8_code(float r) {
-  if (r != r) return 0;
-  r = fminf(fmaxf(r, -127.0f), 127.0f);
-  return (int32_t)r;
+// Rust `x.round() as i32` then clamp to [-127, 127] (NaN -> 0), for the
+// product or quotient x of the quantizer.  round() is half away from zero:
+// trunc(x + copysign(0.5 - 2^-25, x)) in f32 (round-to-nearest-even add)
+// equals it for every f32 x -- checked exhaustively for |x| < 2^23, above
+// which x is an integer that the add leaves unchanged -- and the clamp to
+// integer bounds commutes with the truncation, so the truncating convert
+// finishes it.  ±inf clamp to ±127; NaN gives 0.
+// The add must not fuse with the multiply that produced x (the reference
+// rounds the product first): contraction is off here and in the callers.
+__device__ inline int32_t q8_round_code(float x) {
+#pragma clang fp contract(off)
+  const float y = x + __builtin_copysignf(0x1.fffffep-2f, x);
+  if (y != y) return 0;
+  return (int32_t)fminf(fmaxf(y, -127.0f), 127.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -179,6 +188,7 @@ __device__ inline int32_t q8_code(float r) {
 // block, VPL in {4, 8}); code i of this lane is byte i of the result.
 template <int VPL>
 __device__ inline uint64_t q8_quantize_values(const float *v, int32_t rule, uint16_t &scale) {
+#pragma clang fp contract(off)
   static_assert(VPL == 4 || VPL == 8, "4 or 8 values per lane");
   float amax = 0.0f;
 #pragma unroll
@@ -195,17 +205,47 @@ __device__ inline uint64_t q8_quantize_values(const float *v, int32_t rule, uint
     const float inv = d == 0.0f ? 0.0f : 1.0f / d;
 #pragma unroll
     for (int i = 0; i < VPL; ++i)
-      codes |= ((uint64_t)(uint8_t)(int8_t)q8_code(roundf(v[i] * inv))) << (8 * i);
+      codes |= ((uint64_t)(uint8_t)(int8_t)q8_round_code(v[i] * inv)) << (8 * i);
     scale = f16_rtne(d);
   } else {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int32_t q = d == 0.0f ? 0 : q8_code(roundf(v[i] / d));
+      const int32_t q = d == 0.0f ? 0 : q8_round_code(v[i] / d);
       codes |= ((uint64_t)(uint8_t)(int8_t)q) << (8 * i);
     }
     scale = f16_harserve(d);
   }
   return codes;
+}
+
+// The same rule for a whole 32-value block held by one lane: no shuffles,
+// and the scale's divisions and f16 encoding run once per block.  codes[j]
+// holds codes 4j..4j+3, code i in byte i % 4.
+__device__ inline void q8_quantize_block(const float (&v)[32], int32_t rule, uint16_t &scale,
+                                         uint32_t (&codes)[8]) {
+#pragma clang fp contract(off)
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float x = fabsf(v[i]);
+    amax = x > amax ? x : amax;
+  }
+  const float d = amax == 0.0f ? 0.0f : amax / 127.0f;
+  int32_t q[32];
+  if (rule == 0) {
+    const float inv = d == 0.0f ? 0.0f : 1.0f / d;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) q[i] = q8_round_code(v[i] * inv);
+    scale = f16_rtne(d);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) q[i] = d == 0.0f ? 0 : q8_round_code(v[i] / d);
+    scale = f16_harserve(d);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    codes[j] = ((uint32_t)(uint8_t)q[4 * j]) | ((uint32_t)(uint8_t)q[4 * j + 1] << 8) |
+               ((uint32_t)(uint8_t)q[4 * j + 2] << 16) | ((uint32_t)(uint8_t)q[4 * j + 3] << 24);
 }
 
 __device__ inline uint32_t q8_quantize_lane(const float v[4], int32_t rule, uint16_t &scale) {
