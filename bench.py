@@ -32,6 +32,12 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBS = 8000.0
 
 METRIC = "Q8 paged flash-decode HBM GB/s (% of 8 TB/s) + µs/step at B=64, 32k ctx"
+# The arithmetic a line's kernels compute in.  With a bf16 query, waves of up
+# to 8 rows per kv head take the int8 QK against three int8 query planes;
+# 16-row waves (the verify, the prefill) take the f16 QK.
+DT_INT8_QK = "int8 QK (bf16 query as three int8 planes) + f16 PV (two-term weights), f32 accumulate"
+DT_F16_QK = ("f16 QK (bf16 query exact in f16, K codes widened exactly) + f16 PV (two-term weights), "
+             "f32 accumulate")
 
 
 def load_rkv():
@@ -232,7 +238,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 QK + f16 PV, f32 accumulate",
+        "dtype": DT_INT8_QK,
         "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
         "config": {"workload": f"headline paged Q8 decode step: B={B}, L={L}, Hq={Hq}, Hkv={Hkv}, "
                                f"D={D}, page={PT}, 10% pool slack, bf16 q, f32 out, scale 1/{int(math.sqrt(D))}",
@@ -489,13 +495,13 @@ class _Decoder:
         return int(self.ws[:4 * (1 + 2 * batch)].view(torch.int32)[2::2].sum().item())
 
 
-def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extra):
+def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extra, dtype=DT_INT8_QK):
     value = step_bytes / step_s / 1e9
     res = {
         "metric": f"config {cfg}: paged Q8 decode HBM GB/s (% of 8 TB/s) + us/step",
         "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int8 QK + f16 PV, f32 accumulate",
+        "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
         "config": dict(workload=workload, **extra.pop("config", {})),
         "us_per_step": round(step_s * 1e6, 2),
@@ -660,7 +666,8 @@ def run_config(args) -> int:
                       "pool_pages_per_layer": num_pages, "launch": launch},
            **({"graph_us_per_step": round(graph_wall * 1e6, 2)} if graph_wall else {}),
            "split_k_partial_bytes": n_parts * q_len * Hq * (D + 2) * 4,
-           **({"mean_accept": float(np.mean(accepts))} if accepts else {})})
+           **({"mean_accept": float(np.mean(accepts))} if accepts else {})},
+          dtype=DT_F16_QK if q_len * Hq // Hkv > 8 else DT_INT8_QK)
     pool.close()
     ctx.close()
     return 0
@@ -949,7 +956,7 @@ def run_config7(args) -> int:
         "value": round(flops / wall / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 QK (two q planes) + f16 PV (two-term weights), f32 accumulate",
+        "dtype": DT_F16_QK,
         "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
         "config": {"workload": (f"chunked prefill: B={B} sequences, ctx={C0} cached + {N}-row chunk "
                                 f"each (causal), Hq=16, Hkv=2, D=256, page 64, append + attention "
@@ -1077,7 +1084,8 @@ def run_config9(args) -> int:
         "metric": "config 9: serving step through the adapter, tokens through attention per second",
         "value": round(tokens / wall, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 4), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "int8 QK + f16 PV, f32 accumulate",
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "prefill: " + DT_F16_QK + "; decode (8 rows per kv head): " + DT_INT8_QK,
         "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0; bf16 q)",
         "config": {"workload": f"config 9 serving step (rkv_serve_*): 64 requests, lognormal "
                                f"contexts (median 8192, sigma 1.0, [512, 32768]); per step 8 x "
@@ -1203,7 +1211,7 @@ def run_config10(args) -> int:
         "value": dec["logical_gbs"], "unit": "GB/s", "n_gpus": 1, "steps": reps,
         "warmup": 2, "ms_per_step": round(dec["us"] / 1e3, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 QK (two q planes) + f16 PV (two-term weights), f32 accumulate",
+        "dtype": ("8-row decode: " + DT_INT8_QK + "; 16- and 32-row verify and the prefill: " + DT_F16_QK),
         "data": "synthetic (seeded N(0,1) K/V bf16 -> Q8_0 via the append kernel; bf16 q)",
         "config": {"workload": (f"host-KV tier: B={B}, L={L}, Hq={Hq}, Hkv={Hkv}, D={D}, page {PT}, "
                                 f"pages in pinned host memory ({kv_bytes} K/V bytes); decode, verify "
