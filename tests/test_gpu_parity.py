@@ -278,6 +278,64 @@ def test_append_special_values(rkv, rko, ctx):
         assert np.array_equal(pd.cpu().numpy(), pages), f"rule {rule}"
 
 
+@pytest.mark.parametrize("D,src_bf16", [(128, False), (256, True)])
+def test_append_special_values_large_launch(rkv, rko, ctx, D, src_bf16):
+    """The same special blocks through a launch of 8192 rows x 8 kv heads, which
+    takes the 32-row tiles with one lane per 32-value block (a small launch
+    takes 8-row tiles with four lanes per block): zero, huge, tiny, inf and
+    NaN blocks, the f16 carry window, and exact ties k + 0.5 (amax 127, so
+    d = 1 and v * (1/d) = v) that round half away from zero.  Page bytes
+    equal the oracle's for both rules."""
+    torch = _torch()
+    PT, Hkv, L = 64, 8, 8192
+    NB = D // 32
+    rng = np.random.default_rng(D + 3)
+    rows = rng.standard_normal((L, Hkv, D)).astype(np.float32)
+    blocks = rows.reshape(L, Hkv, NB, 32)
+    kinds = rng.integers(0, 7, (L, Hkv, NB))
+    pick = rng.random((L, Hkv, NB)) < 0.05  # about 5% of the blocks are special
+    ties = (rng.integers(-127, 127, 32) + 0.5).astype(np.float32)
+    ties[0] = 127.0  # amax 127: d = 1 exactly
+    for t in range(7):
+        sel = pick & (kinds == t)
+        if t == 0:
+            blocks[sel] = 0.0
+        elif t == 1:
+            blocks[sel] *= np.float32(3e6)
+        elif t == 2:
+            blocks[sel] *= np.float32(1e-9)
+        elif t == 3:
+            blocks[sel, 5] = np.inf
+        elif t == 4:
+            blocks[sel, 17] = np.nan
+        elif t == 5:
+            blocks[sel] = np.float32(2.0 ** -5 * (2 - 2.0 ** -12) * 127)
+        else:
+            blocks[sel] = ties
+    if src_bf16:
+        src = torch.from_numpy(rows).to(torch.bfloat16)
+        rows = src.float().numpy()  # the values the kernel reads
+    else:
+        src = torch.from_numpy(rows)
+    npg = L // PT
+    bt = rng.permutation(npg + 3)[:npg].astype(np.int32)[None, :]
+    sid = np.zeros(L, np.int32)
+    pos = np.arange(L, dtype=np.int32)
+    sd = src.cuda()
+    for rule in (0, 1):
+        g = rkv.geometry(Hkv, D, PT, npg + 3)
+        lay = rko.layout(Hkv, D, PT, npg + 3)
+        want = np.zeros((npg + 3) * rkv.page_bytes(g), np.uint8)
+        rko.paged_append(lay, want, bt, sid, pos, rows, rows, rule)
+        pd = torch.zeros(want.size, dtype=torch.uint8, device="cuda")
+        rkv.append_q8(ctx, g, pd, torch.from_numpy(bt).cuda(), torch.from_numpy(sid).cuda(),
+                      torch.from_numpy(pos).cuda(), sd, sd, rule=rule)
+        ctx.sync()
+        got = pd.cpu().numpy()
+        bad = np.nonzero(got != want)[0]
+        assert bad.size == 0, f"rule {rule}: {bad.size} bytes differ, first at {bad[:4]}"
+
+
 @pytest.mark.parametrize("D,PT", [(128, 16), (256, 64), (256, 32)])
 def test_import_gather_roundtrip(rkv, rko, ctx, D, PT):
     torch = _torch()
