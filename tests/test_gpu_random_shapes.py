@@ -2,7 +2,8 @@
 the oracle: batch size, lengths (0, 1, page and tile edges included), GQA,
 head_dim, page size, q_len 1..4, explicit or device-chosen partitions,
 f32/bf16 q (the bf16 query takes the f16 QK with 16 or 32 rows per kv head
-and in the prefill), appended rows.  Each case is fixed by its seed, so a failure
+and in the prefill), appended rows; prefill causal ranges whole, split into
+forced segments or split by the automatic plan.  Each case is fixed by its seed, so a failure
 names a reproducible shape.  Bars as in test_gpu_parity.py."""
 import math
 
@@ -89,3 +90,28 @@ def test_random_prefill_shapes(rkv, rko, ctx, seed):
                                 q[None, off:off + n], 1.0 / math.sqrt(D), 1024)[0]
         assert_close(got[off:off + n], want, what=f"seed {seed} entry {i}")
         off += n
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_prefill_split_shapes(rkv, rko, ctx, seed):
+    """Prefill with contexts up to 2000 tokens and the causal ranges split
+    into forced segments (or the automatic plan, or no workspace), mostly with
+    a bf16 query: the pipelined tile loop over whole, partial and empty
+    segments."""
+    from tests import test_gpu_prefill as P
+    rng = np.random.default_rng(5000 + seed)
+    D = int(rng.choice([128, 256]))
+    PT = int(rng.choice([16, 32, 64, 128, 256]))
+    Hkv = int(rng.choice([1, 2]))
+    G = int(rng.choice([1, 2, 4, 8, 16]))
+    n_ent = int(rng.integers(1, 4))
+    ents = [(int(rng.integers(0, 2000)), int(rng.integers(1, 150))) for _ in range(n_ent)]
+    seg = [None, 0, int(max(32, PT) * rng.integers(1, 6))][int(rng.integers(0, 3))]
+    q_bf16 = bool(rng.random() < 0.7)
+    print(f"seed {seed}: D={D} PT={PT} Hkv={Hkv} G={G} entries={ents} segment={seg} bf16 q={q_bf16}",
+          flush=True)
+    lens = [c + n + int(rng.integers(0, 3)) for c, n in ents]
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=seed, src_bf16=True)
+    ent = [(i, c, n) for i, (c, n) in enumerate(ents)]
+    P._run(rkv, rko, ctx, sc, ent, Hkv * G, 1.0 / math.sqrt(D), q_bf16=q_bf16, seed=seed,
+           segment_tokens=seg)
