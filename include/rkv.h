@@ -356,7 +356,13 @@ rkv_status rkv_flash_decode_q8(rkv_ctx *ctx, const rkv_flash_decode_params *p,
 /* ---- pool: device pages for `layers` layers + allocator + device tables ----
  * The operator-level API a serving adapter (BatchStepModel, adapter.rs:28-72)
  * would hold per model.  Block-table edits made through the allocator are
- * uploaded by rkv_pool_sync_tables() before the next launch. */
+ * uploaded by rkv_pool_sync_tables() before the next launch.
+ * A pool's calls that queue device work (sync, append, decode, prefill,
+ * gather, spill, restore) run in call order, whatever streams they are
+ * queued on: a call on another stream than the pool's previous call first
+ * makes its stream wait, on the device, for the work queued so far on that
+ * previous stream (which must still exist then).  Calls on one stream add
+ * nothing. */
 /* Where a pool's pages live.  RKV_PAGES_HOST puts them in pinned host
  * memory mapped for the device (the reference's host-KV tier,
  * research/host-kv/README.md:1-24): every kernel reads and writes them
@@ -386,8 +392,7 @@ rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
  * launches enqueued on `stream` afterwards see the new tables and copied
  * pages, earlier ones the old.  One pinned-staging copy plus one or two
  * small kernels; the host waits only if the staging buffer of the call
- * before last is still in flight.  Use one stream for a pool's syncs and
- * launches. */
+ * before last is still in flight. */
 rkv_status rkv_pool_sync_tables(rkv_pool *pool, void *stream);
 /* Device pointers owned by the pool (for a host-memory pool, the device
  * mapping of its pinned pages). */
@@ -523,7 +528,10 @@ rkv_status rkv_pool_restore(rkv_pool *pool, int32_t seq, const uint8_t *page, si
  *   rkv_serve_begin_step(prefill entries, decode entries)
  *   for each layer: rkv_serve_prefill(...) and/or rkv_serve_decode(...)
  *   (then rkv_serve_truncate / rkv_serve_finish as the step's outcome says;
- *   they take effect at the next rkv_serve_begin_step). */
+ *   they take effect at the next rkv_serve_begin_step).
+ * Steps may change streams: the pool orders its calls whatever streams they
+ * use (rkv_pool_create), and the step's row layout is uploaded behind that
+ * ordering. */
 typedef struct rkv_serve_desc {
   int32_t layers;
   int32_t kv_heads;

@@ -1307,11 +1307,34 @@ struct rkv_pool {
   // R4KV page CRC: device result word and its pinned host copy
   uint32_t *d_crc = nullptr;
   uint32_t *h_crc = nullptr;
+  // the stream of the pool's last call (see order_after_last)
+  hipStream_t last_stream = nullptr;
+  bool has_last = false;
+  hipEvent_t handoff = nullptr;
 };
 
 namespace {
 size_t stage_ints(const rkv_pool_desc &d) {
   return (size_t)d.max_seqs * (d.max_pages_per_seq + 1) + d.max_seqs + 2 * (size_t)d.num_pages;
+}
+
+// A pool's calls run in call order, whatever streams they are queued on.
+// The device tables, lengths and pages are one state: a table sync rewrites
+// the lengths while a decode queued earlier on another stream may still be
+// reading them.  So a call on a stream other than the previous call's first
+// makes its stream wait, on the device, for all the work queued so far on
+// the previous one (an event recorded there; nothing waits on the host).
+// Calls that stay on one stream pay nothing.
+rkv_status order_after_last(rkv_pool *p, hipStream_t hs, const char *op) {
+  if (p->has_last && p->last_stream != hs) {
+    hipError_t e;
+    if ((e = hipEventRecord(p->handoff, p->last_stream)) != hipSuccess ||
+        (e = hipStreamWaitEvent(hs, p->handoff, 0)) != hipSuccess)
+      return hip_fail(op, e);
+  }
+  p->last_stream = hs;
+  p->has_last = true;
+  return RKV_OK;
 }
 }  // namespace
 
@@ -1366,6 +1389,7 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
       (e = hipHostMalloc(&p->h_stage[1], sbytes, hipHostMallocDefault)) != hipSuccess ||
       (e = hipEventCreateWithFlags(&p->stage_done[0], hipEventDisableTiming)) != hipSuccess ||
       (e = hipEventCreateWithFlags(&p->stage_done[1], hipEventDisableTiming)) != hipSuccess ||
+      (e = hipEventCreateWithFlags(&p->handoff, hipEventDisableTiming)) != hipSuccess ||
       (e = hipMalloc(&p->d_crc, 256)) != hipSuccess ||
       (e = hipHostMalloc(&p->h_crc, 256, hipHostMallocDefault)) != hipSuccess) {
     rkv_status s = fail(RKV_ERR_DEVICE, op, "allocating %zu page bytes and tables: %s",
@@ -1408,6 +1432,7 @@ rkv_status rkv_pool_destroy(rkv_pool *p) {
     if (p->h_stage[i]) (void)hipHostFree(p->h_stage[i]);
     if (p->stage_done[i]) (void)hipEventDestroy(p->stage_done[i]);
   }
+  if (p->handoff) (void)hipEventDestroy(p->handoff);
   rkv_alloc_destroy(p->alloc);
   delete p;
   return RKV_OK;
@@ -1426,6 +1451,7 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   // tables and copied pages, and earlier ones the old.  Nothing here waits
   // for the device unless the staging slot's kernels from two syncs ago are
   // still pending.
+  if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
   rkv_alloc *a = p->alloc;
   const int32_t W = a->d.max_pages_per_seq;
   const int32_t S = a->d.max_seqs;
@@ -1474,6 +1500,8 @@ rkv_status rkv_pool_append(rkv_pool *p, int32_t layer, const rkv_append_args *ar
   const char *op = "rkv_pool_append";
   if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
   if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
   return rkv_append_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
                        p->d.max_pages_per_seq, p->d.max_seqs, args, stream);
 }
@@ -1482,6 +1510,8 @@ rkv_status rkv_pool_decode(rkv_pool *p, int32_t layer, const rkv_decode_args *ar
   const char *op = "rkv_pool_decode";
   if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
   if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
   // pages in host memory: K staged through LDS with V (the register loads
   // of K read the host link at 87% of the LDS-DMA copies' rate)
   return decode_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
@@ -1503,6 +1533,8 @@ rkv_status rkv_pool_prefill(rkv_pool *p, int32_t layer, const rkv_prefill_args *
                     e, args->ctx_lens[e], args->q_rows[e], p->alloc->lens[seq], seq);
     }
   }
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
   // pages behind the host link: the row blocks of one causal range share
   // one XCD's L2 (in HBM, chunks of 8 spread them over 4 XCDs)
   return prefill_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
@@ -1517,6 +1549,8 @@ rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind
   if (!p) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
   if (layer < 0 || layer >= p->d.layers) return fail(RKV_ERR_INVALID_ARG, op, "layer=%d", layer);
   if (rkv_status s = check_seq(p->alloc, seq, op)) return s;
+  if (rkv_status s = use_device(p->ctx, op)) return s;
+  if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
   return rkv_gather_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer),
                        p->d_tables + (size_t)seq * p->d.max_pages_per_seq, p->alloc->lens[seq],
                        kind, out, stream);
@@ -1755,6 +1789,7 @@ rkv_status rkv_pool_spill(rkv_pool *p, int32_t seq, int32_t token_start, int32_t
   r.count = token_count;
   rkv_r4kv_header_encode(&h, r.header);
   hipStream_t hs = as_stream(stream);
+  if (rkv_status s = order_after_last(p, hs, op)) return s;
   hipError_t e = rkv::launch_r4kv_pack(r, p->pages, p->d_tables + (size_t)seq * p->d.max_pages_per_seq,
                                        static_cast<uint8_t *>(staging), p->d_crc, p->ctx->d_fault, hs);
   if (e != hipSuccess) return hip_fail(op, e);
@@ -1792,6 +1827,7 @@ rkv_status rkv_pool_restore(rkv_pool *p, int32_t seq, const uint8_t *page, size_
     return fail(RKV_ERR_INVALID_ARG, op, "staging must be 16-byte aligned and hold %zu bytes", body_len);
   const uint32_t stored = get32(page, (int)(RKV_R4KV_HEADER_BYTES + body_len));
   hipStream_t hs = as_stream(stream);
+  if (rkv_status s = order_after_last(p, hs, op)) return s;
   hipError_t e;
   if (body_len > 0 &&
       (e = hipMemcpyAsync(staging, page + RKV_R4KV_HEADER_BYTES, body_len, hipMemcpyHostToDevice, hs)) != hipSuccess)

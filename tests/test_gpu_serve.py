@@ -213,3 +213,55 @@ def test_serve_long_context_chunk_splits(rkv, rko, ctx):
     a = rkv.prefill_args([0], [3000], [64], qt, qt, scale)
     assert rkv.prefill_workspace_bytes(sv.geometry, a) > 0
     sv.close()
+
+
+def test_serve_steps_alternate_streams(rkv, rko, ctx):
+    """Consecutive steps on two streams with no host synchronization between
+    them: each step's row layout is uploaded only after the previous step's
+    launches on the other stream are done with it, so every decode row still
+    matches the oracle."""
+    torch = __import__("torch")
+    D, Hkv, Hq, PT, ctx_len, n_seq, steps = 256, 2, 16, 64, 2048, 4, 6
+    scale = 1.0 / math.sqrt(D)
+    sv = rkv.Serve(ctx, 1, Hkv, D, PT, num_pages=n_seq * (ctx_len // PT + 2) + 8, max_seqs=n_seq,
+                   max_pages_per_seq=ctx_len // PT + 2, q_heads=Hq, max_decode=n_seq,
+                   max_prefill_rows=n_seq * ctx_len, seed=3)
+    m = _Model(rko, 1, Hkv, Hq, D)
+    rng = np.random.default_rng(11)
+    ids = list(range(21, 21 + n_seq))
+    for sid in ids:
+        m.admit(sid)
+    n_pf = n_seq * ctx_len
+    kp = rng.standard_normal((n_pf, Hkv, D)).astype(np.float32)
+    vp = rng.standard_normal((n_pf, Hkv, D)).astype(np.float32)
+    qp = rng.standard_normal((n_pf, Hq, D)).astype(np.float32)
+    op = torch.empty((n_pf, Hq, D), dtype=torch.float32, device="cuda")
+    sv.begin_step(prefill=[(sid, ctx_len) for sid in ids], decode=[])
+    sv.prefill(0, torch.from_numpy(qp).cuda(), torch.from_numpy(kp).cuda(), torch.from_numpy(vp).cuda(),
+               op, scale)
+    ctx.sync()
+    for i, sid in enumerate(ids):
+        m.append(sid, 0, kp[i * ctx_len:(i + 1) * ctx_len], vp[i * ctx_len:(i + 1) * ctx_len])
+    # every step's inputs and outputs staged before the timed-free loop
+    qd = [rng.standard_normal((n_seq, Hq, D)).astype(np.float32) for _ in range(steps)]
+    kd = [rng.standard_normal((n_seq, Hkv, D)).astype(np.float32) for _ in range(steps)]
+    vd = [rng.standard_normal((n_seq, Hkv, D)).astype(np.float32) for _ in range(steps)]
+    dq = [torch.from_numpy(x).cuda() for x in qd]
+    dk = [torch.from_numpy(x).cuda() for x in kd]
+    dv = [torch.from_numpy(x).cuda() for x in vd]
+    od = [torch.zeros((n_seq, Hq, D), dtype=torch.float32, device="cuda") for _ in range(steps)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    print(f"serve: {steps} decode steps alternating two streams, {n_seq} x {ctx_len} tokens", flush=True)
+    for step in range(steps):
+        st = streams[step % 2]
+        sv.begin_step(prefill=[], decode=[(sid, 1) for sid in ids], stream=st)
+        sv.decode(0, dq[step], dk[step], dv[step], od[step], scale, stream=st)
+    torch.cuda.synchronize()
+    for step in range(steps):
+        got = od[step].cpu().numpy()
+        for b, sid in enumerate(ids):
+            m.append(sid, 0, kd[step][b:b + 1], vd[step][b:b + 1])
+            want = m.attend(sid, 0, ctx_len + step + 1, qd[step][b], scale)
+            assert_close(got[b].reshape(-1), want, what=f"step {step} id {sid}")
+    sv.close()
