@@ -1324,12 +1324,20 @@ size_t stage_ints(const rkv_pool_desc &d) {
 // reading them.  So a call on a stream other than the previous call's first
 // makes its stream wait, on the device, for all the work queued so far on
 // the previous one (an event recorded there; nothing waits on the host).
-// Calls that stay on one stream pay nothing.
+// Calls that stay on one stream pay nothing.  A graph capture on either
+// stream is left alone: a capturing stream may neither wait on nor record for
+// work outside its capture, and the stream the graph is launched on orders the
+// captured calls when it runs.
 rkv_status order_after_last(rkv_pool *p, hipStream_t hs, const char *op) {
   if (p->has_last && p->last_stream != hs) {
+    hipStreamCaptureStatus now = hipStreamCaptureStatusNone, before = hipStreamCaptureStatusNone;
     hipError_t e;
-    if ((e = hipEventRecord(p->handoff, p->last_stream)) != hipSuccess ||
-        (e = hipStreamWaitEvent(hs, p->handoff, 0)) != hipSuccess)
+    if ((e = hipStreamIsCapturing(hs, &now)) != hipSuccess ||
+        (e = hipStreamIsCapturing(p->last_stream, &before)) != hipSuccess)
+      return hip_fail(op, e);
+    if (now == hipStreamCaptureStatusNone && before == hipStreamCaptureStatusNone &&
+        ((e = hipEventRecord(p->handoff, p->last_stream)) != hipSuccess ||
+         (e = hipStreamWaitEvent(hs, p->handoff, 0)) != hipSuccess))
       return hip_fail(op, e);
   }
   p->last_stream = hs;
