@@ -270,6 +270,12 @@ def main() -> int:
         res["stream_read_ceiling"] = ceil
         best = max(ceil["vector_gbs"], ceil["lds_dma_gbs"])
         res["roofline"]["frac_of_stream_ceiling"] = round(res["roofline"]["achieved"] / best, 4)
+        # the decode's own tile order over this pool's (shuffled) pages, with
+        # nothing computed: the read rate that access pattern reaches here
+        pat = pattern_ceiling(rkv, ctx, pool, g, B, L, part, pages_per_seq, kv_bytes, stream)
+        res["pattern_read_ceiling"] = pat
+        # K/V bytes over the decode kernel's time against the same bytes over the pattern's
+        res["roofline"]["frac_of_pattern_ceiling"] = round(pat["us"] * 1e-6 / dec_s, 4)
 
     # ---- CPU baseline: the reference path restated in C, timed on a sample -------
     if args.cpu_sample_seqs > 0:
@@ -315,6 +321,30 @@ def stream_ceiling(rkv, ctx, stream, nbytes=4 << 30, reps=5):
     return {"bytes": nbytes, "vector_gbs": round(vec[bv], 1), "vector_blocks": bv,
             "lds_dma_gbs": round(dma[bd], 1), "lds_dma_blocks": bd,
             "kernel": "rkv_stream_read (rkv_stream.hip)"}
+
+
+def pattern_ceiling(rkv, ctx, pool, g, B, L, part, bt_stride, kv_bytes, stream, reps=5):
+    """Read rate of the decode's tile order over the pool's own pages
+    (rkv_stream_read_tiles): the same partitions, 32-token tiles and
+    nontemporal LDS-DMA copies, one tile in flight, no compute; median of
+    `reps` launches after one warm-up."""
+    import torch
+    run = lambda: rkv.stream_read_tiles(ctx, g, pool.layer_pages(0), pool.block_tables_ptr(), bt_stride,
+                                        B, L, part, stream=stream)
+    run()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        run()
+        e1.record(stream)
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e-3)
+    ctx.sync()
+    t = sorted(ts)[len(ts) // 2]
+    return {"gbs": round(kv_bytes / t / 1e9, 1), "us": round(t * 1e6, 2), "bytes": kv_bytes,
+            "kernel": "rkv_stream_read_tiles (rkv_stream.hip): the decode's partitions and 32-token "
+                      "tiles over this pool's pages, nt LDS-DMA copies, one tile in flight, nothing computed"}
 
 
 def read_traffic():

@@ -629,6 +629,22 @@ rkv_status rkv_serve_page_location(const rkv_serve *s, uint64_t id, int32_t ordi
 #define RKV_STREAM_DMA_UNIT 16384
 rkv_status rkv_stream_read(rkv_ctx *ctx, const void *data, uint64_t bytes, int32_t mode,
                            int32_t blocks, uint32_t *out, void *stream);
+/* The decode's tile order over a pool's pages.  No counterpart in the
+ * reference: it gives the practical read rate of the decode's own access
+ * pattern, with the pages wherever the block tables put them, in the same
+ * run.  For n_seqs block-table rows ([n_seqs][bt_stride]) of seq_tokens
+ * tokens each and every kv head, partitions of partition_tokens tokens are
+ * read by one one-wave workgroup each, 32-token tile after tile: its K
+ * codes, V codes and both scale runs, with the decode's nontemporal 1 KiB
+ * LDS-DMA copies and one tile in flight.  Nothing is written.  head_dim 128
+ * or 256, page_tokens >= 32; seq_tokens a multiple of 32; partition_tokens a
+ * multiple of page_tokens of at most 64 pages; the rows must hold
+ * ceil(seq_tokens / page_tokens) pages (a page id outside the pool reads
+ * page 0).  Reads n_seqs * kv_heads * seq_tokens * head_dim * 17/8 bytes.
+ * Stream-ordered. */
+rkv_status rkv_stream_read_tiles(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                                 const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
+                                 int32_t seq_tokens, int32_t partition_tokens, void *stream);
 
 #ifdef __cplusplus
 }

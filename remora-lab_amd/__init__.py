@@ -199,6 +199,8 @@ _SIGS = {
     "rkv_pool_restore": (C.c_int32, [P, C.c_int32, P, C.c_size_t, C.POINTER(R4kvExpect), P,
                                      C.c_size_t, I32P, P]),
     "rkv_stream_read": (C.c_int32, [P, P, C.c_uint64, C.c_int32, C.c_int32, P, P]),
+    "rkv_stream_read_tiles": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, C.c_int32,
+                                          C.c_int32, C.c_int32, P]),
     "rkv_page_generation": (C.c_int32, [P, C.c_int32, C.POINTER(C.c_uint64)]),
     "rkv_serve_create": (C.c_int32, [P, C.POINTER(ServeDesc), C.POINTER(P)]),
     "rkv_serve_destroy": (C.c_int32, [P]),
@@ -484,6 +486,14 @@ def stream_read(ctx: Ctx, data, mode: int, blocks: int, out=None, nbytes=None, s
     n = data.numel() * data.element_size() if nbytes is None else nbytes
     check(lib().rkv_stream_read(ctx.h, _ptr(data), n, mode, blocks,
                                 _ptr(out) if out is not None else None, _stream(stream)))
+
+
+def stream_read_tiles(ctx: Ctx, g: Geometry, pages, block_tables, bt_stride: int, n_seqs: int,
+                      seq_tokens: int, partition_tokens: int, stream=None) -> None:
+    """The decode's tile order over a pool's pages, for its read rate
+    (rkv_stream_read_tiles); reads and discards."""
+    check(lib().rkv_stream_read_tiles(ctx.h, C.byref(g), _ptr(pages), _ptr(block_tables), bt_stride,
+                                      n_seqs, seq_tokens, partition_tokens, _stream(stream)))
 
 
 class R4kvRefused(RkvError):

@@ -161,6 +161,20 @@ hipError_t launch_r4kv_unpack(const R4kvLaunch &r, uint8_t *pages, const int32_t
 hipError_t launch_stream_read(const uint8_t *data, int64_t bytes, int32_t mode, int32_t blocks,
                               uint32_t *out, hipStream_t s);
 int64_t stream_read_dma_unit();
+// The decode's tile order over a pool's pages, for its read rate
+// (rkv_stream_read_tiles): n_seqs block-table rows of seq_tokens tokens,
+// partitions of part_tokens tokens (parts per sequence), each kv head.
+struct TileStreamLaunch {
+  Geo g;
+  const uint8_t *pages;
+  const int32_t *bt;
+  int32_t bt_stride;
+  int32_t n_seqs;
+  int32_t seq_tokens;
+  int32_t part_tokens;
+  int32_t parts;
+};
+hipError_t launch_stream_tiles(const TileStreamLaunch &t, hipStream_t s);
 // the 17..32-row instantiations (own translation unit)
 hipError_t launch_decode_rows32(const DecodeLaunch &d, hipStream_t s);
 

@@ -1650,6 +1650,32 @@ rkv_status rkv_stream_read(rkv_ctx *ctx, const void *data, uint64_t bytes, int32
   return e == hipSuccess ? RKV_OK : hip_fail(op, e);
 }
 
+rkv_status rkv_stream_read_tiles(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
+                                 const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
+                                 int32_t seq_tokens, int32_t partition_tokens, void *stream) {
+  const char *op = "rkv_stream_read_tiles";
+  if (rkv_status s = use_device(ctx, op)) return s;
+  if (rkv_status s = check_geometry(g, op)) return s;
+  if (g->page_tokens < 32) return fail(RKV_ERR_UNSUPPORTED, op, "page_tokens=%d < 32", g->page_tokens);
+  if (!pages || !block_tables) return fail(RKV_ERR_INVALID_ARG, op, "NULL pages/block_tables");
+  if (n_seqs < 1 || seq_tokens < 32 || seq_tokens % 32 != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "n_seqs=%d seq_tokens=%d", n_seqs, seq_tokens);
+  if (partition_tokens < g->page_tokens || partition_tokens % g->page_tokens != 0 ||
+      partition_tokens / g->page_tokens > 64)
+    return fail(RKV_ERR_INVALID_ARG, op, "partition_tokens=%d (page_tokens %d, at most 64 pages)",
+                partition_tokens, g->page_tokens);
+  if ((seq_tokens + g->page_tokens - 1) / g->page_tokens > bt_stride)
+    return fail(RKV_ERR_INVALID_ARG, op, "seq_tokens=%d needs more pages than bt_stride=%d",
+                seq_tokens, bt_stride);
+  const int32_t parts = (seq_tokens + partition_tokens - 1) / partition_tokens;
+  if ((int64_t)n_seqs * parts > INT32_MAX)
+    return fail(RKV_ERR_INVALID_ARG, op, "n_seqs=%d x %d partitions", n_seqs, parts);
+  rkv::TileStreamLaunch t{to_geo(g), static_cast<const uint8_t *>(pages), block_tables, bt_stride,
+                          n_seqs, seq_tokens, partition_tokens, parts};
+  hipError_t e = rkv::launch_stream_tiles(t, as_stream(stream));
+  return e == hipSuccess ? RKV_OK : hip_fail(op, e);
+}
+
 rkv_status rkv_r4kv_header_encode(const rkv_r4kv_header *h, uint8_t out[RKV_R4KV_HEADER_BYTES]) {
   if (!h || !out) return fail(RKV_ERR_INVALID_ARG, "rkv_r4kv_header_encode", "NULL argument");
   std::memset(out, 0, RKV_R4KV_HEADER_BYTES);

@@ -75,11 +75,67 @@ __global__ __launch_bounds__(64) void stream_read_dma_kernel(const uint8_t *p, i
   }
 }
 
+// The decode's tile order over a pool's pages (see launch_stream_tiles):
+// workgroup (entry b's partition, kv head) reads each 32-token tile of its
+// partition as the decode stages it -- K codes, V codes (D/32 KiB each) and
+// both scale runs (2*D bytes each, one copy) -- with nontemporal 1 KiB
+// LDS-DMA copies, waits for them, and moves to the next tile.
+template <int D>
+__global__ __launch_bounds__(64) void stream_tiles_kernel(TileStreamLaunch t) {
+  constexpr int kCodeCopies = D / 32;  // 1 KiB copies per code run of a tile
+  constexpr int kCopies = 2 * kCodeCopies + 1;
+  __shared__ __attribute__((aligned(1024))) uint8_t st[2][kCopies * 1024];
+  const Geo g = t.g;
+  const int lane = threadIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.x / t.parts, part = blockIdx.x % t.parts;
+  const int32_t tok0 = part * t.part_tokens;
+  const int32_t tok_end = min(t.seq_tokens, tok0 + t.part_tokens);
+  const int n_tiles = (tok_end - tok0) / 32;
+  const int pg0 = tok0 / g.page_tokens;
+  const int npg = (tok_end - tok0 + g.page_tokens - 1) / g.page_tokens;
+  int32_t pid = lane < npg ? t.bt[(int64_t)b * t.bt_stride + pg0 + lane] : 0;
+  if (pid < 0 || pid >= g.num_pages) pid = 0;  // every copy stays inside the pool
+  const uint64_t RB = region_bytes(g), PB = page_bytes(g);
+  const uint32_t PTD = (uint32_t)g.page_tokens * D;
+  // the scale copy: lanes [0, D/8) K scales, [D/8, D/4) V scales, the rest
+  // re-read the K scales' first chunk
+  const uint32_t sc_off = lane < D / 8 ? PTD + 16u * lane
+                                       : (lane < D / 4 ? (uint32_t)RB + PTD + 16u * (lane - D / 8) : PTD);
+  for (int i = 0; i < n_tiles; ++i) {
+    const int32_t s0 = (i * 32) % g.page_tokens;
+    const int32_t p = __builtin_amdgcn_readlane(pid, (i * 32) / g.page_tokens);
+    const uint8_t *kb = t.pages + (uint64_t)p * PB + (uint64_t)(2 * kvh) * RB;
+    uint8_t *dst = st[i & 1];
+#pragma unroll
+    for (int c = 0; c < kCodeCopies; ++c) {
+      __builtin_amdgcn_global_load_lds(kb + (uint64_t)s0 * D + 1024 * c + 16 * lane,
+                                       (__attribute__((address_space(3))) void *)(dst + 1024 * c), 16, 0, kNT);
+      __builtin_amdgcn_global_load_lds(kb + RB + (uint64_t)s0 * D + 1024 * c + 16 * lane,
+                                       (__attribute__((address_space(3))) void *)(dst + 1024 * (kCodeCopies + c)),
+                                       16, 0, kNT);
+    }
+    __builtin_amdgcn_global_load_lds(kb + sc_off + (uint64_t)s0 * (D / 16),
+                                     (__attribute__((address_space(3))) void *)(dst + 1024 * (2 * kCodeCopies)),
+                                     16, 0, kNT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+}
+
 __global__ void clear_word_kernel(uint32_t *w) { *w = 0u; }
 
 }  // namespace
 
 int64_t stream_read_dma_unit() { return 1024LL * kDmaLoads; }
+
+hipError_t launch_stream_tiles(const TileStreamLaunch &t, hipStream_t s) {
+  const dim3 grid((unsigned)(t.n_seqs * t.parts), (unsigned)t.g.kv_heads);
+  if (t.g.head_dim == 256)
+    hipLaunchKernelGGL(stream_tiles_kernel<256>, grid, dim3(64), 0, s, t);
+  else
+    hipLaunchKernelGGL(stream_tiles_kernel<128>, grid, dim3(64), 0, s, t);
+  return hipGetLastError();
+}
 
 hipError_t launch_stream_read(const uint8_t *data, int64_t bytes, int32_t mode, int32_t blocks,
                               uint32_t *out, hipStream_t s) {

@@ -35,3 +35,35 @@ def test_dma_mode_runs_and_bad_args_are_refused(rkv, ctx):
         with pytest.raises(rkv.RkvError):
             rkv.stream_read(ctx, d, mode, nb, out, nbytes=nbytes)
     ctx.sync()
+
+
+def test_tile_order_read_runs_and_bad_args_are_refused(rkv, ctx):
+    """rkv_stream_read_tiles walks a pool's pages through its block tables
+    in the decode's tile order; it writes nothing, reports no fault, and
+    refuses shapes it does not cover."""
+    import torch
+    for D, PT in [(256, 64), (128, 32), (256, 256)]:
+        print(f"tile-order read D={D} page {PT}", flush=True)
+        Hkv, B, L = 2, 3, 4096
+        npg = L // PT
+        num_pages = B * npg + 5
+        g = rkv.geometry(Hkv, D, PT, num_pages)
+        pages = torch.zeros(num_pages * rkv.page_bytes(g), dtype=torch.uint8, device="cuda")
+        perm = np.random.default_rng(D + PT).permutation(num_pages)[:B * npg]
+        bt = torch.from_numpy(perm.reshape(B, npg).astype(np.int32)).cuda()
+        bt[1, 3] = num_pages + 7  # outside the pool: read as page 0
+        before = pages.clone()
+        rkv.stream_read_tiles(ctx, g, pages, bt, npg, B, L, min(64 * PT, 1024))
+        ctx.sync()
+        assert torch.equal(pages, before)
+    for bt_stride, n, L, part in [(npg, B, L + 16, 1024),   # not a multiple of 32
+                                  (npg, B, L, 48),          # not a multiple of page_tokens
+                                  (npg, B, L, 64 * PT * 2),  # more than 64 pages
+                                  (npg - 1, B, L, 1024),     # rows too short
+                                  (npg, 0, L, 1024)]:        # no sequences
+        with pytest.raises(rkv.RkvError):
+            rkv.stream_read_tiles(ctx, g, pages, bt, bt_stride, n, L, part)
+    g16 = rkv.geometry(Hkv, 256, 16, num_pages)
+    with pytest.raises(rkv.RkvError):  # 16-token pages are not covered
+        rkv.stream_read_tiles(ctx, g16, pages, bt, npg, B, L, 256)
+    ctx.sync()
