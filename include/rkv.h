@@ -305,7 +305,12 @@ rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pa
                           const rkv_prefill_args *args, void *stream);
 /* Workspace bytes the split of these arguments uses: with segment_tokens > 0
  * that split, with 0 the split chosen when the workspace is large enough
- * (0 when none is); the device pointers in args are not read. */
+ * (0 when none is); with a bf16 query (q_dtype) also room for every tile of
+ * the entries' causal ranges widened once (head_dim * 132 bytes, padded to
+ * whole KiB, per 32 tokens and kv head), which the prefill then copies
+ * instead of widening it in each of the row blocks that read it.  A smaller
+ * workspace still works: the tiles are widened per row block.  The device
+ * pointers in args are not read. */
 size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_args *args);
 
 /* Export seq's K or V cache in the reference contiguous layout

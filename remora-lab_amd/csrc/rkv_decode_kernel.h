@@ -1292,6 +1292,64 @@ struct Decoder {
     if (t < n_tiles) pipe_step(t, r0, r1, f0, f1);
   }
 
+  // Tiles widened once (PrefillLaunch::pre): tile t's image (kPBytes: K and
+  // V f16, K scales, V scales, as the compute reads them) is copied from the
+  // unit's run of images in the workspace straight into f16 buffer t % 3,
+  // two tiles ahead of the compute; nothing is widened here.
+  static constexpr int kPBytes = (int)prefill_tile_bytes(D);
+  static constexpr int kPCopies = kPBytes / 1024;  // 1 KiB copies per tile
+  static constexpr int kPVS = 130 * D;             // V scales in the image
+  const uint8_t *pre_src;                          // the unit's first tile image
+  __device__ __forceinline__ void issue_pre(int tile, lds_u8 *dst) {
+    static_assert(kPipe, "widened tiles feed the f16 compute");
+    const uint8_t *src = pre_src + (uint64_t)tile * kPBytes + 16 * lane;
+    // this wave's copies k = i*NW + wave; re-read by every row block of the
+    // range, so the default cache policy
+#pragma unroll
+    for (int i = 0; i < (kPCopies + NW - 1) / NW; ++i) {
+      const int k = i * NW + swave;
+      if (kPCopies % NW != 0 && k >= kPCopies) break;
+      __builtin_amdgcn_global_load_lds(src + 1024 * k, dst + 1024 * k, 16, 0, 0);
+    }
+  }
+  // Step t with widened tiles: tile t in fc (copied two steps ago), fn the
+  // buffer of tile t-1, which tile t+2 refills.  One barrier: after it every
+  // wave's copies of tile t have landed and every wave is done with fn.
+  __device__ __forceinline__ void pre_step(int t, lds_u8 *__restrict__ fc, lds_u8 *__restrict__ fn) {
+    // this wave's copies of tile t; tile t+1's (the floor of kPCopies / NW
+    // of them, one more on some waves) may stay in flight
+    if (t + 1 < n_tiles) {
+      constexpr int n = kPCopies / NW;
+      __builtin_amdgcn_s_waitcnt(kWaitBase | (n & 0xf) | ((n >> 4) << 14));
+    } else {
+      __builtin_amdgcn_s_waitcnt(kWaitBase);
+    }
+    wg_barrier_lds();
+    if (t + 2 < n_tiles) issue_pre(t + 2, fn);
+    // tile t's V scales into this wave's vsc, with the accumulators' 2^vexp
+    // step (scale_v reads them at S::kVS of the pointer it is given); the
+    // widening pass zeroed the scales past the entry's end
+    scale_v(fc + kPVS - S::kVS);
+    kf16 = fc + kFK;
+    vf16 = fc + kFV;
+    ks = fc + kFS;
+    compute(t, fc);  // reads fc and vsc only
+  }
+  __device__ __forceinline__ void run_pre(lds_u8 *__restrict__ f0, lds_u8 *__restrict__ f1,
+                                          lds_u8 *__restrict__ f2) {
+    if (n_tiles == 0) return;
+    issue_pre(0, f0);
+    if (n_tiles > 1) issue_pre(1, f1);
+    int t = 0;
+    for (; t + 2 < n_tiles; t += 3) {
+      pre_step(t, f0, f2);
+      pre_step(t + 1, f1, f0);
+      pre_step(t + 2, f2, f1);
+    }
+    if (t < n_tiles) pre_step(t, f0, f2);
+    if (t + 1 < n_tiles) pre_step(t + 1, f1, f0);
+  }
+
   __device__ __forceinline__ void step(int t, const lds_u8 *cur, lds_u8 *fill) {
     if constexpr (kKReg) {
       // tile t's K codes and stage copy were the last loads issued

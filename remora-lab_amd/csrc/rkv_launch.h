@@ -133,8 +133,20 @@ struct PrefillLaunch {
   int32_t xcd_chunk;  // 1: plain round robin; more: row blocks of one range share an L2
   float *ws_ml;  // split partials: (m, l) [partial row][2] ...
   float *ws_o;   // ... and o [partial row][head_dim]
+  // Tiles widened once (bf16 query): the widening pass writes every 32-token
+  // tile of every entry's causal range, per kv head, as the image the
+  // compute reads from LDS (prefill_tile_bytes each, K and V as f16 and
+  // both scale runs); the prefill copies those images instead of widening
+  // per workgroup.  Entry k's tiles start at tile index preoff[k] (kv head h:
+  // + h * tiles of the entry); preoff[n_entries] is the total.  nullptr: the
+  // workgroups widen their tiles themselves.
+  uint8_t *pre;
+  int64_t preoff[kPrefillMaxEntries + 1];
 };
 hipError_t launch_prefill(const PrefillLaunch &pf, hipStream_t s);
+// bytes of one widened tile image: K and V f16 (64*D each), the K and V
+// scale runs (2*D each), padded to whole 1 KiB copies
+constexpr int64_t prefill_tile_bytes(int head_dim) { return (132LL * head_dim + 1023) / 1024 * 1024; }
 
 // CRC32C of n bytes at `data` (16-byte aligned, device-readable) into *out
 // (device word), stream-ordered; the word is cleared by the launch itself.

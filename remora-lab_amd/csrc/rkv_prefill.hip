@@ -26,17 +26,23 @@ namespace {
 // kQF16: a bf16 query, whose QK runs on f16 MFMA against K codes the
 // workgroup widens once per tile (Decoder kF16K); an f32 query keeps the
 // int8 QK with three query planes.
-template <int D, bool kSmall, int NS, bool kQF16>
+// kPre (with kQF16): the tiles come widened from the widening pass
+// (PrefillLaunch::pre) and are copied into three f16 buffers; no stage ring
+// and no page list.
+template <int D, bool kSmall, int NS, bool kQF16, bool kPre = false>
 __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_kernel(PrefillLaunch pf) {
 #if defined(__HIP_DEVICE_COMPILE__)
+  static_assert(!kPre || kQF16, "widened tiles feed the f16 QK");
   using Dec = Decoder<D, 2, kSmall, NS, kPrefillWaves, true, true, false, kQF16>;
   using S = StageShape<D>;
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[NS][S::kAlloc];
-  __shared__ int32_t page_list[kPrefillMaxPages];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kPre ? 1 : NS][kPre ? 1024 : S::kAlloc];
+  __shared__ int32_t page_list[kPre ? 1 : kPrefillMaxPages];
   // kQF16: two f16 buffers, each a tile's K and V widened and its K scales
   // (Decoder::run_pipe widens tile t+1 into one while tile t is computed from
-  // the other); otherwise the tile's V as f16
-  __shared__ __attribute__((aligned(16))) uint8_t f16buf[kQF16 ? 2 * Dec::kFBytes : D * 64];
+  // the other); kPre: three buffers of copied tile images; otherwise the
+  // tile's V as f16
+  __shared__ __attribute__((aligned(1024))) uint8_t
+      f16buf[kPre ? 3 * Dec::kPBytes : (kQF16 ? 2 * Dec::kFBytes : D * 64)];
   __shared__ __attribute__((aligned(16))) uint8_t v_scl[kPrefillWaves * 2 * D];  // each wave's scaled V scales
   const DecodeLaunch &p = pf.d;
   const Geo g = p.g;
@@ -87,16 +93,18 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
     return;
   }
   // the unit's page ids; bad entries are reported and replaced by page 0 so
-  // every copy stays inside the pool
-  for (int32_t i = threadIdx.x; i < npg; i += 64 * kPrefillWaves) {
-    int32_t pid = p.bt[(int64_t)seq * p.bt_stride + pg0 + i];
-    if (pid < 0 || pid >= g.num_pages) {
-      atomicOr(p.fault, FAULT_BAD_PAGE);
-      pid = 0;
+  // every copy stays inside the pool (kPre: the widening pass did that)
+  if constexpr (!kPre) {
+    for (int32_t i = threadIdx.x; i < npg; i += 64 * kPrefillWaves) {
+      int32_t pid = p.bt[(int64_t)seq * p.bt_stride + pg0 + i];
+      if (pid < 0 || pid >= g.num_pages) {
+        atomicOr(p.fault, FAULT_BAD_PAGE);
+        pid = 0;
+      }
+      page_list[i] = pid;
     }
-    page_list[i] = pid;
+    __syncthreads();
   }
-  __syncthreads();
 
   Dec dc(p);
   dc.lane = threadIdx.x & 63;
@@ -149,7 +157,12 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
   dc.PB = page_bytes(g);
   dc.kv_base = p.pages + (uint64_t)kvh * 2u * region_bytes(g);
 
-  if constexpr (kQF16) {
+  if constexpr (kPre) {
+    // entry e's images: kv head after kv head, each its causal range's tiles
+    const int64_t tiles_e = ((int64_t)ctx + n + kTile - 1) / kTile;
+    dc.pre_src = pf.pre + (uint64_t)(pf.preoff[e] + kvh * tiles_e + tok0 / kTile) * Dec::kPBytes;
+    dc.run_pre((lds_u8 *)f16buf, (lds_u8 *)f16buf + Dec::kPBytes, (lds_u8 *)f16buf + 2 * Dec::kPBytes);
+  } else if constexpr (kQF16) {
     static_assert(NS == 2, "the pipelined prefill runs a two-stage ring");
     dc.run_pipe((lds_u8 *)lds[0], (lds_u8 *)lds[1], (lds_u8 *)f16buf, (lds_u8 *)f16buf + Dec::kFBytes);
   } else {
@@ -174,6 +187,104 @@ __global__ __launch_bounds__(64 * kPrefillWaves, kPrefillWgsPerCu) void prefill_
         *reinterpret_cast<v4f *>(pf.ws_o + prow * D + 16 * m + 4 * lg) = dc.oacc[0][m];
       if (lg == 0) *reinterpret_cast<float2 *>(pf.ws_ml + 2 * prow) = float2{dc.mref[0], l};
     }
+  }
+#endif  // __HIP_DEVICE_COMPILE__
+}
+
+// The widening pass (PrefillLaunch::pre): one 256-thread workgroup per
+// (entry, kv head, 32-token tile of the entry's causal range [0, ctx+rows)),
+// in the order of the images: entry by entry (launch order), kv head by kv
+// head, tile by tile.  It writes the tile as the f16 compute reads it from
+// LDS (Decoder kFK/kFV/kFS, what widen_k, widen_v and widen_into produce
+// from a staged tile), plus the V scales at kPVS:
+//  - K: token row r as exact f16, 16-byte chunk c of the row at
+//    c ^ (r mod D/8);
+//  - V: chunk (dim d, k-group g) = the 8 tokens 4g..4g+3, 16+4g..16+4g+3 of
+//    dim d as exact f16 (the codes are stored biased), at slot g ^ (d & 3);
+//  - scales: each run [block][32 positions] in the staged order (position q
+//    of a block holds token tok32(q)), V scales past the entry's end zeroed.
+// Every tile is read from its pages once, instead of once per row block.
+__device__ __forceinline__ int tok32(int q) {
+  const int lg = q >> 3, i = (q >> 1) & 3;
+  return (i < 2 ? 0 : 16) + 4 * lg + 2 * (i & 1) + (q & 1);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void widen_tiles_kernel(PrefillLaunch pf) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  using Dec = Decoder<D, 2, false, 2, kPrefillWaves, true, true, false, true>;
+  const DecodeLaunch &p = pf.d;
+  const Geo g = p.g;
+  const int64_t x = blockIdx.x;
+  if (x >= pf.preoff[pf.n_entries]) return;
+  int e = 0;
+  while (e + 1 < pf.n_entries && x >= pf.preoff[e + 1]) ++e;
+  const int32_t len = pf.ctx[e] + pf.rows[e];
+  const int64_t tiles = ((int64_t)len + kTile - 1) / kTile;
+  const int64_t v = x - pf.preoff[e];
+  const int kvh = (int)(v / tiles);
+  const int32_t j = (int32_t)(v % tiles);
+  const int32_t seq = pf.seq[e];
+  uint8_t *dst = pf.pre + (uint64_t)x * Dec::kPBytes;
+  const int tid = threadIdx.x;
+  if (seq < 0 || seq >= p.n_seqs) return;  // the prefill kernel reports it
+  // page of tile token r (r < 32); bad ids are reported and read as page 0.
+  // Tokens past the entry's end read the tile's first token instead (with
+  // 16-token pages the second half may have no page); their V scales are
+  // zeroed below and the causal mask drops their scores.
+  auto page_of = [&](int r, int32_t &slot) -> int32_t {
+    const int32_t pos = j * kTile + r < len ? j * kTile + r : j * kTile;
+    slot = pos % g.page_tokens;
+    int32_t pid = p.bt[(int64_t)seq * p.bt_stride + pos / g.page_tokens];
+    if (pid < 0 || pid >= g.num_pages) {
+      atomicOr(p.fault, FAULT_BAD_PAGE);
+      pid = 0;
+    }
+    return pid;
+  };
+  // K: 32 rows x D/16 chunks of 16 codes
+  for (int c = tid; c < 32 * (D / 16); c += 256) {
+    const int r = c / (D / 16), lc = c % (D / 16);
+    int32_t slot;
+    const int32_t pid = page_of(r, slot);
+    const v4i w = *reinterpret_cast<const v4i *>(p.pages + region_base(g, pid, kvh, 0) +
+                                                 code_offset(g, 0, slot, 16 * lc));
+    v2h h[8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v8x4_to_f16((uint32_t)w[q] ^ 0x80808080u, h[2 * q], h[2 * q + 1]);
+    const v8h f0 = {h[0][0], h[0][1], h[1][0], h[1][1], h[2][0], h[2][1], h[3][0], h[3][1]};
+    const v8h f1 = {h[4][0], h[4][1], h[5][0], h[5][1], h[6][0], h[6][1], h[7][0], h[7][1]};
+    uint8_t *row = dst + Dec::kFK + r * (2 * D);
+    *reinterpret_cast<v8h *>(row + 16 * ((2 * lc) ^ (r & (D / 8 - 1)))) = f0;
+    *reinterpret_cast<v8h *>(row + 16 * ((2 * lc + 1) ^ (r & (D / 8 - 1)))) = f1;
+  }
+  // V: chunks (d, g), 4 consecutive tokens of each 16-token half
+  for (int c = tid; c < 4 * D; c += 256) {
+    const int d = c >> 2, gq = c & 3;
+    uint32_t w[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      int32_t slot;
+      const int32_t pid = page_of(16 * hf + 4 * gq, slot);
+      w[hf] = *reinterpret_cast<const uint32_t *>(p.pages + region_base(g, pid, kvh, 1) +
+                                                  code_offset(g, 1, slot, d));
+    }
+    v2h a0, a1, a2, a3;
+    v8x4_to_f16(w[0], a0, a1);
+    v8x4_to_f16(w[1], a2, a3);
+    const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+    *reinterpret_cast<v8h *>(dst + Dec::kFV + 16 * (4 * d + (gq ^ (d & 3)))) = va;
+  }
+  // scales: kind, block, position
+  for (int c = tid; c < 2 * D; c += 256) {
+    const int kind = c / D, b = (c % D) / 32, q = c % 32;
+    const int t = tok32(q);
+    int32_t slot;
+    const int32_t pid = page_of(t, slot);
+    uint16_t sc = *reinterpret_cast<const uint16_t *>(p.pages + region_base(g, pid, kvh, kind) +
+                                                      scale_offset(g, slot, b));
+    if (kind == 1 && j * kTile + t >= len) sc = 0;  // past the entry's end: junk
+    *reinterpret_cast<uint16_t *>(dst + (kind == 0 ? Dec::kFS : Dec::kPVS) + 2 * (32 * b + q)) = sc;
   }
 #endif  // __HIP_DEVICE_COMPILE__
 }
@@ -240,7 +351,11 @@ hipError_t launch_prefill_t(const PrefillLaunch &pf, hipStream_t s) {
   const int64_t round = 8 * (int64_t)std::max(pf.xcd_chunk, 1);
   dim3 grid((unsigned)((units + round - 1) / round * round));
   const bool small = pf.d.g.page_tokens < kTile, qf16 = pf.d.q_bf16 != 0;
-  if (small && qf16)
+  if (pf.pre != nullptr && qf16) {
+    // widen every tile once, then copy the images
+    hipLaunchKernelGGL(widen_tiles_kernel<D>, dim3((unsigned)pf.preoff[pf.n_entries]), dim3(256), 0, s, pf);
+    hipLaunchKernelGGL((prefill_kernel<D, false, NS, true, true>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
+  } else if (small && qf16)
     hipLaunchKernelGGL((prefill_kernel<D, true, NS, true>), grid, dim3(64 * kPrefillWaves), 0, s, pf);
   else if (small)
     hipLaunchKernelGGL((prefill_kernel<D, true, NS, false>), grid, dim3(64 * kPrefillWaves), 0, s, pf);

@@ -680,6 +680,17 @@ size_t prefill_ws_bytes(int64_t partial_rows, int32_t head_dim) {
   return ml + (size_t)partial_rows * head_dim * 4;
 }
 
+// Widened tile images (PrefillLaunch::pre) of a bf16-query prefill: one per
+// (entry, kv head, 32-token tile of [0, ctx + rows)), after the partials at
+// a 1 KiB boundary.
+size_t prefill_pre_bytes(const rkv_kv_geometry *g, int32_t n, const int32_t *ctx_lens,
+                         const int32_t *q_rows) {
+  int64_t tiles = 0;
+  for (int32_t e = 0; e < n; ++e) tiles += ((int64_t)ctx_lens[e] + q_rows[e] + 31) / 32;
+  return (size_t)tiles * g->kv_heads * (size_t)rkv::prefill_tile_bytes(g->head_dim);
+}
+size_t prefill_pre_at(size_t partial_bytes) { return (partial_bytes + 1023) / 1024 * 1024; }
+
 constexpr int64_t kUnitCost = 64;       // tokens: a unit's prologue and epilogue
 constexpr int64_t kSplitUnitCost = 32;  // tokens: a split unit's partial rows
 constexpr int64_t kMaxSimUnits = 16384; // units (times kv heads) a plan simulates at most
@@ -817,7 +828,7 @@ SegPlan plan_segments(const rkv_kv_geometry *g, int32_t q_heads, int32_t tq, int
 rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                         const int32_t *bt, int32_t bt_stride, int32_t n_seqs,
                         const rkv_prefill_args *a, const char *op, int32_t xcd_chunk,
-                        rkv::PrefillLaunch &pf) {
+                        bool widen_once, rkv::PrefillLaunch &pf) {
   if (rkv_status s = check_geometry(g, op)) return s;
   if (rkv_status s = check_tables(pages, bt, bt_stride, n_seqs, op)) return s;
   if (!a) return fail(RKV_ERR_INVALID_ARG, op, "args is NULL");
@@ -891,6 +902,27 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
     pf.ws_o = reinterpret_cast<float *>(static_cast<uint8_t *>(a->workspace) +
                                         ws_need - (size_t)prow * g->head_dim * 4);
   }
+  // a bf16 query whose workspace also holds every tile widened: the widening
+  // pass runs once per tile and the prefill copies the images; otherwise
+  // each workgroup widens the tiles it reads.  Not for pages in host memory:
+  // there the pass would read every page over the link before the prefill
+  // starts (measured 1.30 ms against 0.73-0.77 for a 512-row chunk after
+  // 32768 tokens), where the row blocks' reads overlap their compute.
+  pf.pre = nullptr;
+  if (widen_once && a->q_dtype == RKV_BF16 && a->workspace && a->n_seqs > 0) {
+    const size_t at = prefill_pre_at(ws_need);
+    const size_t need = prefill_pre_bytes(g, a->n_seqs, a->ctx_lens, a->q_rows);
+    if (need > 0 && a->workspace_bytes >= at + need) {
+      pf.pre = static_cast<uint8_t *>(a->workspace) + at;
+      int64_t t = 0;
+      for (int32_t k = 0; k < a->n_seqs; ++k) {
+        pf.preoff[k] = t;
+        t += ((int64_t)pf.ctx[k] + pf.rows[k] + 31) / 32 * g->kv_heads;
+      }
+      pf.preoff[a->n_seqs] = t;
+      if (t > INT32_MAX) pf.pre = nullptr;  // one widening workgroup per image
+    }
+  }
   pf.first[a->n_seqs] = (int32_t)blocks;
   pf.xcd_chunk = xcd_chunk;
   if (blocks > 0 && (!a->q || !a->out)) return fail(RKV_ERR_INVALID_ARG, op, "NULL q/out");
@@ -918,12 +950,13 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
 
 rkv_status prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pages,
                       const int32_t *block_tables, int32_t bt_stride, int32_t n_seqs,
-                      const rkv_prefill_args *a, void *stream, int32_t xcd_chunk) {
+                      const rkv_prefill_args *a, void *stream, int32_t xcd_chunk,
+                      bool widen_once = true) {
   const char *op = "rkv_prefill_q8";
   if (rkv_status s = use_device(ctx, op)) return s;
   rkv::PrefillLaunch pf{};
   if (rkv_status s =
-          make_prefill(ctx, g, pages, block_tables, bt_stride, n_seqs, a, op, xcd_chunk, pf))
+          make_prefill(ctx, g, pages, block_tables, bt_stride, n_seqs, a, op, xcd_chunk, widen_once, pf))
     return s;
   hipError_t e = rkv::launch_prefill(pf, as_stream(stream));
   return e == hipSuccess ? RKV_OK : hip_fail(op, e);
@@ -950,7 +983,9 @@ size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_a
     if (a->ctx_lens[e] < 0 || a->q_rows[e] < 0) return 0;
   const SegPlan sp = plan_segments(g, a->q_heads, rkv::kPrefillRows / G, a->n_seqs, a->ctx_lens,
                                    a->q_rows, a->segment_tokens, SIZE_MAX, rkv::kPrefillXcdChunkHbm);
-  return prefill_ws_bytes(sp.partial_rows, g->head_dim);
+  const size_t partials = prefill_ws_bytes(sp.partial_rows, g->head_dim);
+  if (a->q_dtype != RKV_BF16) return partials;
+  return prefill_pre_at(partials) + prefill_pre_bytes(g, a->n_seqs, a->ctx_lens, a->q_rows);
 }
 
 rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
@@ -1545,10 +1580,11 @@ rkv_status rkv_pool_prefill(rkv_pool *p, int32_t layer, const rkv_prefill_args *
   if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
   // pages behind the host link: the row blocks of one causal range share
   // one XCD's L2 (in HBM, chunks of 8 spread them over 4 XCDs)
+  // (and no widening pass, which would read every page over the link first)
+  const bool host = p->d.page_memory == RKV_PAGES_HOST;
   return prefill_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
                     p->d.max_pages_per_seq, p->d.max_seqs, args, stream,
-                    p->d.page_memory == RKV_PAGES_HOST ? rkv::kPrefillXcdChunkHost
-                                                       : rkv::kPrefillXcdChunkHbm);
+                    host ? rkv::kPrefillXcdChunkHost : rkv::kPrefillXcdChunkHbm, !host);
 }
 
 rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind, uint8_t *out,
