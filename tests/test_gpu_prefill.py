@@ -272,3 +272,44 @@ def test_pool_chunked_prefill_then_decode(rkv, rko, ctx):
     ctx.sync()
     assert_close(o.cpu().numpy()[0, 0], outs[layers - 1][299], what="decode vs prefill row")
     pool.close()
+
+
+def test_prefill_widened_once_matches_per_block(rkv, rko, ctx):
+    """A bf16 query with the full workspace widens each tile once into it;
+    a workspace that holds only the split partials (what an f32 query asks
+    for) and no workspace at all widen per row block instead.  All three
+    give the oracle's rows, and the split runs agree to 1e-5."""
+    torch = _torch()
+    Hq, Hkv, D, PT = 16, 2, 256, 64
+    entries = [(0, 700, 130), (1, 33, 64), (2, 0, 45)]
+    sc = Scene(rkv, rko, Hkv, D, PT, [c + n for _, c, n in entries], seed=21)
+    rng = np.random.default_rng(22)
+    total = sum(n for _, _, n in entries)
+    q = rko.bf16_to_f32(rko.f32_to_bf16(
+        outlier_q(rng, (total, Hq, D)))).reshape(total, Hq, D)
+    qd = torch.from_numpy(q).cuda().to(torch.bfloat16)
+    cols = ([s for s, _, _ in entries], [c for _, c, _ in entries], [n for _, _, n in entries])
+    scale = 1.0 / np.sqrt(D)
+    q32 = torch.zeros((total, Hq, D), device="cuda")
+    partials = rkv.prefill_workspace_bytes(
+        sc.g, rkv.prefill_args(*cols, q32, torch.zeros_like(q32), scale))
+    full = rkv.prefill_workspace_bytes(
+        sc.g, rkv.prefill_args(*cols, qd, torch.zeros_like(q32), scale))
+    assert full >= partials + 3 * Hkv * 132 * D  # at least one widened tile per entry
+    outs = {}
+    for name, nb in (("full", full), ("partials", partials), ("none", None)):
+        out = torch.full((total, Hq, D), float("nan"), device="cuda")
+        ws = None if not nb else torch.empty(nb, dtype=torch.uint8, device="cuda")
+        a = rkv.prefill_args(*cols, qd, out, scale, segment_tokens=0 if ws is not None else -1,
+                             workspace=ws)
+        rkv.prefill_q8(ctx, sc.g, sc.pages_d, sc.bt_d, len(entries), a)
+        ctx.sync()
+        outs[name] = out.cpu().numpy()
+    off = 0
+    for s, c, n in entries:
+        want = _oracle(rko, sc, s, c, n, q[off:off + n], scale)
+        for name, got in outs.items():
+            assert_close(got[off:off + n], want, what=f"{name}: seq {s} ctx {c} rows {n}")
+        off += n
+    if partials:
+        assert float(np.abs(outs["full"] - outs["partials"]).max()) <= 1e-5
