@@ -995,7 +995,11 @@ def run_config7(args) -> int:
                    "segment_tokens": args.prefill_segment, "split_workspace_bytes": ws_bytes},
         "us_per_step": round(wall * 1e6, 2),
         "flops_per_step": flops,
-        "roofline": {"bound": "mfma", "kernel": "rkv::prefill_kernel<256, false, 2>",
+        # events bracket the whole rkv_pool_prefill call: with a bf16 query and a
+        # workspace that holds the widened tiles, the widening pass plus the
+        # prefill kernel (and the split combine when the launch splits)
+        "roofline": {"bound": "mfma", "kernel": ("rkv::widen_tiles_kernel<256> + "
+                                                 "rkv::prefill_kernel<256, false, 2, true, true>"),
                      "achieved": round(flops / kern / 1e12, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(flops / kern / 1e12 / peak, 4), "traffic": None,
                      "prefill_us": round(kern * 1e6, 2)},
