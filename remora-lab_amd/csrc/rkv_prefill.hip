@@ -228,19 +228,33 @@ __global__ __launch_bounds__(256) void widen_tiles_kernel(PrefillLaunch pf) {
   uint8_t *dst = pf.pre + (uint64_t)x * Dec::kPBytes;
   const int tid = threadIdx.x;
   if (seq < 0 || seq >= p.n_seqs) return;  // the prefill kernel reports it
-  // page of tile token r (r < 32); bad ids are reported and read as page 0.
-  // Tokens past the entry's end read the tile's first token instead (with
-  // 16-token pages the second half may have no page); their V scales are
-  // zeroed below and the causal mask drops their scores.
-  auto page_of = [&](int r, int32_t &slot) -> int32_t {
-    const int32_t pos = j * kTile + r < len ? j * kTile + r : j * kTile;
-    slot = pos % g.page_tokens;
+  // The tile's two 16-token halves each lie inside one page (page_tokens is a
+  // multiple of 16).  Their page ids are looked up once; bad ids are reported
+  // and read as page 0.  A half that starts past the entry's end (possible
+  // only for the second: the tile's first token is inside the range) reads
+  // the first half's page instead, since with 16-token pages it may have none.
+  int32_t hpid[2], hslot[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int32_t pos = j * kTile + 16 * h < len ? j * kTile + 16 * h : j * kTile;
+    hslot[h] = pos % g.page_tokens;
     int32_t pid = p.bt[(int64_t)seq * p.bt_stride + pos / g.page_tokens];
     if (pid < 0 || pid >= g.num_pages) {
-      atomicOr(p.fault, FAULT_BAD_PAGE);
+      if (tid == 0) atomicOr(p.fault, FAULT_BAD_PAGE);
       pid = 0;
     }
-    return pid;
+    hpid[h] = pid;
+  }
+  // page and slot of tile token r (r < 32).  Tokens past the entry's end read
+  // the tile's first token (written data: its K scale is finite); their V
+  // scales are zeroed below and the causal mask drops their scores.
+  auto page_of = [&](int r, int32_t &slot) -> int32_t {
+    if (j * kTile + r < len) {
+      slot = hslot[r >> 4] + (r & 15);
+      return hpid[r >> 4];
+    }
+    slot = hslot[0];
+    return hpid[0];
   };
   // K: 32 rows x D/16 chunks of 16 codes
   for (int c = tid; c < 32 * (D / 16); c += 256) {
@@ -258,22 +272,24 @@ __global__ __launch_bounds__(256) void widen_tiles_kernel(PrefillLaunch pf) {
     *reinterpret_cast<v8h *>(row + 16 * ((2 * lc) ^ (r & (D / 8 - 1)))) = f0;
     *reinterpret_cast<v8h *>(row + 16 * ((2 * lc + 1) ^ (r & (D / 8 - 1)))) = f1;
   }
-  // V: chunks (d, g), 4 consecutive tokens of each 16-token half
-  for (int c = tid; c < 4 * D; c += 256) {
-    const int d = c >> 2, gq = c & 3;
-    uint32_t w[2];
+  // V: one dim per thread, each half's 16 codes of the dim in one 16-byte
+  // load (the V codes of a dim are contiguous within a 16-token half, at a
+  // 16-byte aligned offset); chunk (d, g) takes tokens 4g..4g+3 of each half.
+  // Codes past the entry's end are finite junk under zeroed V scales.
+  for (int d = tid; d < D; d += 256) {
+    v4i w[2];
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
-      int32_t slot;
-      const int32_t pid = page_of(16 * hf + 4 * gq, slot);
-      w[hf] = *reinterpret_cast<const uint32_t *>(p.pages + region_base(g, pid, kvh, 1) +
-                                                  code_offset(g, 1, slot, d));
+    for (int h = 0; h < 2; ++h)
+      w[h] = *reinterpret_cast<const v4i *>(p.pages + region_base(g, hpid[h], kvh, 1) +
+                                            code_offset(g, 1, hslot[h], d));
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      v2h a0, a1, a2, a3;
+      v8x4_to_f16((uint32_t)w[0][gq], a0, a1);
+      v8x4_to_f16((uint32_t)w[1][gq], a2, a3);
+      const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+      *reinterpret_cast<v8h *>(dst + Dec::kFV + 16 * (4 * d + (gq ^ (d & 3)))) = va;
     }
-    v2h a0, a1, a2, a3;
-    v8x4_to_f16(w[0], a0, a1);
-    v8x4_to_f16(w[1], a2, a3);
-    const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-    *reinterpret_cast<v8h *>(dst + Dec::kFV + 16 * (4 * d + (gq ^ (d & 3)))) = va;
   }
   // scales: kind, block, position
   for (int c = tid; c < 2 * D; c += 256) {
