@@ -214,7 +214,9 @@ typedef struct rkv_prefill_args {
   int32_t total_rows;       /* rows of q and out */
   const void *q;            /* device [total_rows][q_heads][head_dim], 16-byte aligned */
   int32_t q_dtype;          /* RKV_F32 | RKV_BF16 */
-  int32_t q_heads;          /* multiple of kv_heads; q_heads/kv_heads divides 128 */
+  int32_t q_heads;          /* multiple of kv_heads, q_heads/kv_heads <= 128; a row
+                               block takes floor(128/(q_heads/kv_heads)) chunk
+                               tokens of all the kv head's q heads */
   float scale;              /* softmax scale on q.k */
   void *out;                /* device [total_rows][q_heads][head_dim] */
   int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
@@ -541,10 +543,14 @@ typedef struct rkv_serve_desc {
   int32_t layers;
   int32_t kv_heads;
   int32_t head_dim;
-  int32_t page_tokens;        /* the scheduler's page_size (scheduler.rs:1045-1052) */
-  int32_t num_pages;
+  int32_t page_tokens;        /* the scheduler's page_size (scheduler.rs:1045-1052;
+                                 ServeConfig::default() has 8, :103-120): a power
+                                 of two, 1..256.  The pool's pages hold whole
+                                 scheduler pages: page_tokens tokens when that
+                                 is 16 or more, else 32 (rkv_serve_geometry) */
+  int32_t num_pages;          /* scheduler pages the pool holds */
   int32_t max_seqs;           /* live sequences at once */
-  int32_t max_pages_per_seq;
+  int32_t max_pages_per_seq;  /* scheduler pages of one sequence */
   int32_t q_heads;            /* multiple of kv_heads */
   int32_t max_decode;         /* decode rows per step, 1..max_seqs */
   int32_t max_prefill_rows;   /* prefill query rows per step, >= 0 */
@@ -565,23 +571,32 @@ typedef struct rkv_serve_entry {
 } rkv_serve_entry;
 
 /* Where one KV page record lives: the ExactHotQ8 representation's
- * PhysicalPageLocation (har-kv/src/page.rs:100-115) for page `ordinal` of a
- * sequence, i.e. tokens [ordinal*page_tokens, (ordinal+1)*page_tokens), all
- * layers and kv heads (the KVPageId of scheduler.rs:1056-1066).  Layer l's
- * bytes are at offset + l*layer_stride in the pool's page memory
- * (rkv_pool_layer_pages(pool, 0)). */
+ * PhysicalPageLocation (har-kv/src/page.rs:100-115) for scheduler page
+ * `ordinal` of a sequence, i.e. tokens [ordinal*page_tokens,
+ * (ordinal+1)*page_tokens), all layers and kv heads (the KVPageId of
+ * scheduler.rs:1056-1066).  The record is slots [first_slot, first_slot +
+ * slots) of pool page `page`, whose bytes (all its slots) are at offset +
+ * l*layer_stride for layer l in the pool's page memory
+ * (rkv_pool_layer_pages(pool, 0)); a page's slots are not contiguous bytes
+ * (K rows, V columns and scales are separate runs), so a record smaller
+ * than its pool page names the page and its slots. */
 typedef struct rkv_page_location {
   int32_t page;           /* pool page id */
   uint64_t offset;        /* bytes from the start of a layer's page array */
   uint64_t length;        /* page bytes of one layer (rkv_page_bytes) */
   uint64_t layer_stride;  /* bytes between layers' page arrays */
   uint64_t generation;    /* rkv_page_generation of the page */
+  int32_t first_slot;     /* the record's first token slot in the page */
+  int32_t slots;          /* the record's tokens (page_tokens of the desc) */
 } rkv_page_location;
 
 typedef struct rkv_serve rkv_serve;
 rkv_status rkv_serve_create(rkv_ctx *ctx, const rkv_serve_desc *desc, rkv_serve **out);
 rkv_status rkv_serve_destroy(rkv_serve *s);
 rkv_pool *rkv_serve_pool(rkv_serve *s);
+/* The pool's geometry: kv heads, head_dim, tokens of a pool page (see
+ * rkv_serve_desc.page_tokens) and pool pages per layer. */
+rkv_status rkv_serve_geometry(const rkv_serve *s, rkv_kv_geometry *out);
 /* Admit ids seen for the first time (forking those with fork_len > 0), grow
  * every entry's sequence by its tokens and upload the tables and the step's
  * row layout, ordered on `stream`.  An id appears at most once per step;

@@ -118,7 +118,8 @@ class ServeEntry(C.Structure):
 
 class PageLocation(C.Structure):
     _fields_ = [("page", C.c_int32), ("offset", C.c_uint64), ("length", C.c_uint64),
-                ("layer_stride", C.c_uint64), ("generation", C.c_uint64)]
+                ("layer_stride", C.c_uint64), ("generation", C.c_uint64),
+                ("first_slot", C.c_int32), ("slots", C.c_int32)]
 
 
 class PoolDesc(C.Structure):
@@ -205,6 +206,7 @@ _SIGS = {
     "rkv_serve_create": (C.c_int32, [P, C.POINTER(ServeDesc), C.POINTER(P)]),
     "rkv_serve_destroy": (C.c_int32, [P]),
     "rkv_serve_pool": (P, [P]),
+    "rkv_serve_geometry": (C.c_int32, [P, C.POINTER(Geometry)]),
     "rkv_serve_begin_step": (C.c_int32, [P, C.POINTER(ServeEntry), C.c_int32,
                                          C.POINTER(ServeEntry), C.c_int32, P]),
     "rkv_serve_decode": (C.c_int32, [P, C.c_int32, P, P, P, C.c_int32, P, C.c_int32,
@@ -724,9 +726,14 @@ class Serve:
         check(lib().rkv_serve_create(ctx.h, C.byref(d), C.byref(h)))
         self.h = h
         self.desc = d
-        self.geometry = Geometry(kv_heads, head_dim, page_tokens, num_pages)
+        # the pool's own geometry: scheduler pages below 16 tokens share
+        # 32-token pool pages
+        self.geometry = Geometry()
+        check(lib().rkv_serve_geometry(h, C.byref(self.geometry)))
         self.pool_h = P(lib().rkv_serve_pool(h))
-        self.alloc = Allocator(num_pages, page_tokens, max_seqs, max_pages_per_seq,
+        per = self.geometry.page_tokens // page_tokens
+        self.alloc = Allocator(self.geometry.num_pages, self.geometry.page_tokens, max_seqs,
+                               (max_pages_per_seq + per - 1) // per,
                                handle=P(lib().rkv_pool_allocator(self.pool_h)))
 
     def begin_step(self, prefill=(), decode=(), stream=None) -> None:

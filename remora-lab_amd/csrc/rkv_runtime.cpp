@@ -838,9 +838,14 @@ rkv_status make_prefill(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *page
   if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0)
     return fail(RKV_ERR_INVALID_ARG, op, "q_heads=%d is not a multiple of kv_heads=%d",
                 a->q_heads, g->kv_heads);
+  // a row block holds tq = floor(128 / G) chunk tokens times the G q heads
+  // of its kv head; a group that does not divide 128 (the reference's
+  // default 24 q / 4 kv heads, attention.rs:134-137, leaves 2 of the 128
+  // rows) runs the rows past tq * G as dead rows, as a chunk's last block
+  // runs those past its last token
   const int32_t G = a->q_heads / g->kv_heads;
-  if (rkv::kPrefillRows % G != 0)
-    return fail(RKV_ERR_UNSUPPORTED, op, "q_heads/kv_heads=%d does not divide %d", G,
+  if (G > rkv::kPrefillRows)
+    return fail(RKV_ERR_UNSUPPORTED, op, "q_heads/kv_heads=%d exceeds %d rows per block", G,
                 rkv::kPrefillRows);
   if (a->q_dtype != RKV_F32 && a->q_dtype != RKV_BF16)
     return fail(RKV_ERR_UNSUPPORTED, op, "q_dtype=%d", a->q_dtype);
@@ -978,7 +983,7 @@ size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_a
   if (a->n_seqs < 1 || a->n_seqs > RKV_PREFILL_MAX_SEQS || !a->ctx_lens || !a->q_rows) return 0;
   if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0) return 0;
   const int32_t G = a->q_heads / g->kv_heads;
-  if (rkv::kPrefillRows % G != 0) return 0;
+  if (G > rkv::kPrefillRows) return 0;
   for (int32_t e = 0; e < a->n_seqs; ++e)
     if (a->ctx_lens[e] < 0 || a->q_rows[e] < 0) return 0;
   const SegPlan sp = plan_segments(g, a->q_heads, rkv::kPrefillRows / G, a->n_seqs, a->ctx_lens,

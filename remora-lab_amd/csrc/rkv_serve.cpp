@@ -33,8 +33,10 @@ struct rkv_serve {
   rkv_ctx *ctx = nullptr;
   rkv_serve_desc d{};
   rkv_pool *pool = nullptr;
-  rkv_kv_geometry g{};
+  rkv_kv_geometry g{};  // the pool's physical geometry
   size_t page_bytes = 0;
+  int32_t per_page = 1;  // the scheduler's pages (KV page records) per pool page
+  int32_t row_pages = 0; // pool pages of a block-table row
   std::unordered_map<uint64_t, int32_t> slot_of;  // live SequenceId -> pool sequence
   std::vector<int32_t> free_slots;                 // unused pool sequences, a stack
   // the step begun last
@@ -87,13 +89,35 @@ rkv_status rkv_serve_create(rkv_ctx *ctx, const rkv_serve_desc *desc, rkv_serve 
                 desc->max_decode, desc->max_seqs, desc->max_prefill_rows);
   if (desc->rule != RKV_Q8_CANONICAL && desc->rule != RKV_Q8_HARSERVE)
     return fail(RKV_ERR_INVALID_ARG, op, "rule=%d", desc->rule);
-  rkv_pool_desc pd{desc->layers,    desc->kv_heads, desc->head_dim,
-                   desc->page_tokens, desc->num_pages, desc->max_seqs,
-                   desc->max_pages_per_seq, desc->free_list_seed, desc->page_memory};
+  // The scheduler's page (attach_page_if_boundary, scheduler.rs:1045-1077;
+  // ServeConfig::default() page_size 8, :103-120) is a record of
+  // page_tokens tokens.  Pool pages hold whole records: a record of 16
+  // tokens or more is one pool page; smaller records (1, 2, 4, 8) share
+  // 32-token pool pages, which the kernels read as one 32-token tile (the
+  // page of KVGeometry::qwen36_27b, har-kv/src/geometry.rs:39-59).
+  const int32_t lpt = desc->page_tokens;
+  if (lpt < 1 || lpt > 256 || (lpt & (lpt - 1)) != 0)
+    return fail(RKV_ERR_UNSUPPORTED, op, "page_tokens=%d (a power of two, 1..256)", lpt);
+  if (desc->num_pages < 1 || desc->max_pages_per_seq < 1)
+    return fail(RKV_ERR_INVALID_ARG, op, "num_pages=%d max_pages_per_seq=%d", desc->num_pages,
+                desc->max_pages_per_seq);
+  const int32_t ppt = lpt >= 16 ? lpt : 32;
+  const int32_t per = ppt / lpt;
+  rkv_pool_desc pd{desc->layers,
+                   desc->kv_heads,
+                   desc->head_dim,
+                   ppt,
+                   (int32_t)(((int64_t)desc->num_pages + per - 1) / per),
+                   desc->max_seqs,
+                   (int32_t)(((int64_t)desc->max_pages_per_seq + per - 1) / per),
+                   desc->free_list_seed,
+                   desc->page_memory};
   rkv_serve *s = new rkv_serve;
   s->ctx = ctx;
   s->d = *desc;
-  s->g = rkv_kv_geometry{desc->kv_heads, desc->head_dim, desc->page_tokens, desc->num_pages};
+  s->per_page = per;
+  s->row_pages = pd.max_pages_per_seq;
+  s->g = rkv_kv_geometry{desc->kv_heads, desc->head_dim, ppt, pd.num_pages};
   if (rkv_status st = rkv_pool_create(ctx, &pd, &s->pool)) {
     delete s;
     return st;
@@ -106,7 +130,7 @@ rkv_status rkv_serve_create(rkv_ctx *ctx, const rkv_serve_desc *desc, rkv_serve 
   a.batch = desc->max_decode;
   a.q_len = 1;
   a.q_heads = desc->q_heads;
-  a.max_seq_len = desc->max_pages_per_seq * desc->page_tokens;
+  a.max_seq_len = pd.max_pages_per_seq * ppt;
   s->ws_bytes = rkv_decode_workspace_bytes(&s->g, &a);
   // prefill partials: about two units of 128 rows per workgroup slot, which
   // the automatic split (about one unit per slot) fits in; layout (m, l)
@@ -371,6 +395,12 @@ rkv_status rkv_serve_seq_slot(const rkv_serve *s, uint64_t id, int32_t *slot) {
   return live_slot(s, id, "rkv_serve_seq_slot", slot);
 }
 
+rkv_status rkv_serve_geometry(const rkv_serve *s, rkv_kv_geometry *out) {
+  if (!s || !out) return fail(RKV_ERR_INVALID_ARG, "rkv_serve_geometry", "NULL argument");
+  *out = s->g;
+  return RKV_OK;
+}
+
 rkv_status rkv_serve_page_location(const rkv_serve *s, uint64_t id, int32_t ordinal,
                                    rkv_page_location *out) {
   const char *op = "rkv_serve_page_location";
@@ -378,18 +408,29 @@ rkv_status rkv_serve_page_location(const rkv_serve *s, uint64_t id, int32_t ordi
   if (rkv_status st = live_slot(s, id, op, &slot)) return st;
   if (!out) return fail(RKV_ERR_INVALID_ARG, op, "out is NULL");
   const rkv_alloc *a = rkv_pool_allocator(s->pool);
-  std::vector<int32_t> row(s->d.max_pages_per_seq);
+  int32_t len = 0;
+  if (rkv_status st = rkv_seq_len(a, slot, &len)) return st;
+  // records that hold at least one of the sequence's tokens
+  const int32_t lpt = s->d.page_tokens;
+  const int32_t records = (int32_t)(((int64_t)len + lpt - 1) / lpt);
+  if (ordinal < 0 || ordinal >= records)
+    return fail(RKV_ERR_INVALID_ARG, op, "page ordinal %d outside [0, %d) of id %llu", ordinal,
+                records, (unsigned long long)id);
+  std::vector<int32_t> row((size_t)s->row_pages);
   int32_t held = 0;
   if (rkv_status st = rkv_block_table_get(a, slot, row.data(), (int32_t)row.size(), &held))
     return st;
-  if (ordinal < 0 || ordinal >= held)
-    return fail(RKV_ERR_INVALID_ARG, op, "page ordinal %d outside [0, %d) of id %llu", ordinal,
-                held, (unsigned long long)id);
-  out->page = row[ordinal];
-  out->offset = (uint64_t)row[ordinal] * s->page_bytes;
+  const int32_t k = ordinal / s->per_page;
+  if (k >= held)  // the allocator holds ceil(len / pool page) pages
+    return fail(RKV_ERR_INVALID_ARG, op, "pool page %d of id %llu not held", k,
+                (unsigned long long)id);
+  out->page = row[k];
+  out->offset = (uint64_t)row[k] * s->page_bytes;
   out->length = s->page_bytes;
-  out->layer_stride = (uint64_t)s->d.num_pages * s->page_bytes;
-  return rkv_page_generation(a, row[ordinal], &out->generation);
+  out->layer_stride = (uint64_t)s->g.num_pages * s->page_bytes;
+  out->first_slot = (ordinal % s->per_page) * lpt;
+  out->slots = lpt;
+  return rkv_page_generation(a, row[k], &out->generation);
 }
 
 }  // extern "C"

@@ -385,6 +385,12 @@ def test_config1_decode(rkv, rko, ctx):
     # a few tokens each: the outlier channels (|v| up to ~30) are averaged
     # over almost nothing, so every weight's rounding shows
     (16, 2, 256, 64, [2, 3, 5, 9, 17, 40], True, False),
+    # the reference's own geometry: FlashDecodeParams::default() 24 q / 4 kv
+    # heads (attention.rs:134-137), KVGeometry::qwen36_27b D 256 with
+    # 32-token pages (har-kv/src/geometry.rs:39-59): 6 rows per kv head
+    (24, 4, 256, 32, [3000, 517, 33, 1, 1200], True, False),
+    (24, 4, 256, 32, [2100, 64, 7], False, False),
+    (24, 4, 256, 32, [900, 31], True, True),
 ])
 def test_decode_parity(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_bf16, out_bf16):
     print(f"decode Hq={Hq} Hkv={Hkv} D={D} PT={PT} lens={lens}", flush=True)
@@ -451,6 +457,15 @@ def outlier_q(rng, shape):
     (16, 2, 128, 32, [1200, 64], True, 2),
     # 32 rows: the two-wave causal verify
     (16, 2, 256, 64, [1504, 74, 37], True, 4),
+    # the reference's 24 q / 4 kv heads on 32-token pages: 6 rows (q_len 1),
+    # 12 rows (q_len 2), 18 and 24 rows (the two-wave verify, q_len 3 and 4)
+    (24, 4, 256, 32, [2500, 40, 999], True, 1),
+    (24, 4, 256, 32, [1700, 5, 640], False, 1),
+    (24, 4, 256, 32, [1800, 65], True, 2),
+    (24, 4, 256, 32, [1300, 77, 5], False, 2),
+    (24, 4, 256, 32, [1100, 300, 40], True, 3),
+    (24, 4, 256, 32, [1504, 74, 37], True, 4),
+    (24, 4, 256, 32, [900, 33], False, 4),
 ])
 def test_decode_outlier_query(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_bf16, q_len):
     """Queries with outlier channels (x32 and x100) against the reference's
@@ -560,6 +575,10 @@ def test_splitk_partials_and_combine(rkv, rko, ctx):
     (16, 2, 256, 64, [200, 100, 7], 3, 0, False),
     # explicit partitions, bf16 out
     (32, 4, 256, 32, [900, 129], 4, 512, True),
+    # the reference's 24 q / 4 kv heads: 24 rows (8 dead rows in the second
+    # wave's n-tile), device-chosen and explicit partitions
+    (24, 4, 256, 32, [1100, 129, 3], 4, 0, False),
+    (24, 4, 256, 32, [700, 300], 4, 256, True),
 ])
 def test_verify_bf16_query_shapes(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, out_bf16):
     """17..32 rows per kv head with a bf16 query: the two waves split the head
@@ -773,6 +792,10 @@ def _last_rows(sc, b, q_len):
     (16, 4, 128, 32, [514, 300, 4, 1030, 35], 4, 512, 0, False),
     # device-chosen partitions (the last partition takes a one-tile remainder)
     (16, 2, 256, 64, [4097, 66, 300, 12000], 1, 0, 1, False),
+    # the reference's 24 q / 4 kv heads on 32-token pages: 6, 12 and 24 rows
+    (24, 4, 256, 32, [2049, 33, 40, 700], 1, 0, 0, True),
+    (24, 4, 256, 32, [1030, 64, 5], 2, 512, 1, True),
+    (24, 4, 256, 32, [2049, 33, 40], 4, 1024, 0, True),
 ])
 def test_append_in_decode(rkv, rko, ctx, Hq, Hkv, D, PT, lens, q_len, part, rule, src_bf16):
     """The decode launch's own append (rkv_decode_args.append) writes the same

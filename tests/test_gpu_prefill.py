@@ -86,6 +86,13 @@ def _run(rkv, rko, ctx_h, sc, entries, Hq, scale, q_bf16=False, out_bf16=False, 
     # bf16 q (the f16 QK) on 16-token pages, D = 128 and 256
     (8, 2, 128, 16, [(0, 33), (200, 100), (31, 2)], True, True, 0.0),
     (16, 2, 256, 16, [(0, 40), (90, 33), (517, 16)], True, False, 0.01),
+    # the reference's 24 q / 4 kv heads (G = 6, which does not divide 128:
+    # 21 chunk tokens per row block, rows 126 and 127 dead) on 32-token pages
+    (24, 4, 256, 32, [(0, 40), (300, 21), (129, 128), (64, 1), (1000, 70)], True, False, 0.01),
+    (24, 4, 256, 32, [(0, 43), (200, 100), (31, 2)], False, False, 0.0),
+    # G = 3 (42 tokens per block) and G = 12 (10 tokens per block)
+    (12, 4, 128, 32, [(7, 130), (500, 42)], True, False, 0.0),
+    (24, 2, 256, 64, [(100, 95), (0, 11)], True, True, 0.0),
 ])
 def test_prefill_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16, out_bf16, outliers):
     lens = [c + n + extra for (c, n), extra in zip(entries, [3, 0, 5, 0, 2])]
@@ -120,6 +127,8 @@ def test_prefill_outlier_query(rkv, rko, ctx, Hq, Hkv, D, PT, entries, q_bf16):
     # 256-token pages (segment rounded up to a page), G = 1 and G = 16
     (16, 16, 128, 256, [(700, 150), (0, 7)], 100, False),
     (32, 2, 128, 64, [(1500, 23), (0, 9)], 512, True),
+    # the reference's 24 q / 4 kv heads on 32-token pages
+    (24, 4, 256, 32, [(1000, 70), (0, 40), (300, 21)], 96, False),
 ])
 def test_prefill_split_parity(rkv, rko, ctx, Hq, Hkv, D, PT, entries, seg, out_bf16):
     """Row blocks' causal ranges split into segments whose partials the
@@ -212,9 +221,9 @@ def test_prefill_rejects_bad_arguments(rkv, rko, ctx):
     with pytest.raises(rkv.RkvError) as e:
         call([0], [0], [4], offs=[6])                      # offset + rows > total rows
     assert e.value.status == rkv.ERR_INVALID_ARG
-    q12 = torch.zeros((8, 24, D), device="cuda")           # 12 q heads per kv head
+    qbig = torch.zeros((8, 2 * 130, D), device="cuda")     # 130 q heads per kv head
     with pytest.raises(rkv.RkvError) as e:
-        call([0], [0], [4], qq=q12, oo=torch.zeros_like(q12))
+        call([0], [0], [4], qq=qbig, oo=torch.zeros_like(qbig))
     assert e.value.status == rkv.ERR_UNSUPPORTED
     many = rkv.PREFILL_MAX_SEQS + 1
     with pytest.raises(rkv.RkvError) as e:
@@ -274,13 +283,25 @@ def test_pool_chunked_prefill_then_decode(rkv, rko, ctx):
     pool.close()
 
 
-def test_prefill_widened_once_matches_per_block(rkv, rko, ctx):
+@pytest.mark.parametrize("Hq,Hkv,D,PT", [
+    (16, 2, 256, 64),
+    # 16-token pages: the widening pass looks up each 16-token half's page;
+    # the ranges of entries 1 and 2 end inside the first half of their last
+    # tile, whose second half then has no page
+    (16, 2, 256, 16),
+    (8, 2, 128, 16),
+    # the reference's 24 q / 4 kv heads on 32-token pages
+    (24, 4, 256, 32),
+])
+def test_prefill_widened_once_matches_per_block(rkv, rko, ctx, Hq, Hkv, D, PT):
     """A bf16 query with the full workspace widens each tile once into it;
     a workspace that holds only the split partials (what an f32 query asks
     for) and no workspace at all widen per row block instead.  All three
     give the oracle's rows, and the split runs agree to 1e-5."""
     torch = _torch()
-    Hq, Hkv, D, PT = 16, 2, 256, 64
+    print(f"widened once Hq={Hq} Hkv={Hkv} D={D} PT={PT}", flush=True)
+    # causal ranges 830 (ends in the second 16-token half of its last tile),
+    # 97 and 45 (end in the first half)
     entries = [(0, 700, 130), (1, 33, 64), (2, 0, 45)]
     sc = Scene(rkv, rko, Hkv, D, PT, [c + n for _, c, n in entries], seed=21)
     rng = np.random.default_rng(22)
