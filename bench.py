@@ -51,12 +51,103 @@ def load_rkv():
     return mod
 
 
+class GpuState:
+    """The GPU's graphics and memory clocks and its socket power, sampled
+    through amdsmi on a side thread every `period` seconds while a timed
+    region runs, plus its power cap and clock limits: so that a line from a
+    slower-clocked or power-capped box can be told apart from a slower
+    build.  Any amdsmi failure is reported in the result, never raised."""
+
+    def __init__(self, period=0.02):
+        import threading
+        self.period, self.samples, self.static, self.error = period, [], {}, None
+        self._stop = threading.Event()
+        self._thread = None
+        self.h = None
+        try:
+            import amdsmi
+            self.smi = amdsmi
+            amdsmi.amdsmi_init()
+            hs = amdsmi.amdsmi_get_processor_handles()
+            self.h = hs[0] if len(hs) == 1 else self._match(hs)
+            gfx = amdsmi.amdsmi_get_clock_info(self.h, amdsmi.AmdSmiClkType.GFX)
+            mem = amdsmi.amdsmi_get_clock_info(self.h, amdsmi.AmdSmiClkType.MEM)
+            cap = amdsmi.amdsmi_get_power_cap_info(self.h)
+            self.static = {"gfx_clk_max_mhz": gfx.get("max_clk"), "mem_clk_max_mhz": mem.get("max_clk"),
+                           "power_cap_w": self._watts(cap.get("power_cap")),
+                           "default_power_cap_w": self._watts(cap.get("default_power_cap"))}
+        except Exception as e:  # no amdsmi, no permission, no device
+            self.error = f"{type(e).__name__}: {e}"
+
+    def _match(self, hs):
+        import torch
+        bus = torch.cuda.get_device_properties(0).pci_bus_id
+        for h in hs:
+            if int(self.smi.amdsmi_get_gpu_device_bdf(h).split(":")[1], 16) == bus:
+                return h
+        return hs[0]
+
+    @staticmethod
+    def _watts(v):
+        if not isinstance(v, (int, float)):
+            return None
+        return round(v / 1e6, 1) if v > 1e5 else v  # amdsmi reports caps in microwatts
+
+    def _one(self):
+        smi = self.smi
+        try:
+            g = smi.amdsmi_get_clock_info(self.h, smi.AmdSmiClkType.GFX).get("clk")
+            m = smi.amdsmi_get_clock_info(self.h, smi.AmdSmiClkType.MEM).get("clk")
+            w = smi.amdsmi_get_power_info(self.h).get("current_socket_power")
+            self.samples.append((g, m, w))
+            return True
+        except Exception as e:
+            self.error = f"{type(e).__name__}: {e}"
+            return False
+
+    def _sample(self):
+        while not self._stop.wait(self.period) and self._one():
+            pass
+
+    def start(self):
+        """One sample now (the warm-up has just run), then one every period."""
+        import threading
+        if self.h is not None and self.error is None and self._one():
+            self._thread = threading.Thread(target=self._sample, daemon=True)
+            self._thread.start()
+        return self
+
+    def stop(self) -> dict:
+        """Stop sampling, with one last sample (a short region may end before
+        the first period)."""
+        import numpy as np
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+            self._one()
+        res = dict(self.static)
+        if self.samples:
+            for i, k in enumerate(("gfx_clk_mhz", "mem_clk_mhz", "socket_power_w")):
+                xs = [x[i] for x in self.samples if isinstance(x[i], (int, float))]
+                if xs:
+                    res[k + "_p10_p50_p90"] = [float(v) for v in np.percentile(xs, [10, 50, 90])]
+            res["samples"] = len(self.samples)
+        if self.error:
+            res["error"] = self.error
+        return res
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--event-every", type=int, default=5,
                     help="record the per-kernel HIP events on every N-th timed step")
+    ap.add_argument("--event-steps", type=int, default=24,
+                    help="steps of the event pass after the timed region, each with its per-kernel "
+                         "events, that the percentiles are taken from (at least 20)")
+    ap.add_argument("--no-secondary", dest="secondary", action="store_false",
+                    help="headline only: skip configs 2, 3 and 5 in the default line")
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=32768)
@@ -194,11 +285,26 @@ def main() -> int:
         for x in e:
             x.record(stream)
     torch.cuda.synchronize()
+    gpu = GpuState().start()
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(evs.get(i))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    gpu_state = gpu.stop()
+    ctx.sync()
+    # the event pass: every step with its events (markers cost the stream a
+    # few us per step, so it runs after the timed region), for percentiles
+    # over at least 20 samples
+    n_pass = max(args.event_steps, 20)
+    pass_evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(n_pass)]
+    for e in pass_evs:
+        for x in e:
+            x.record(stream)
+    torch.cuda.synchronize()
+    for e in pass_evs:
+        step(e)
+    torch.cuda.synchronize()
     ctx.sync()
     part = int(ws[:4].view(torch.int32).item())  # the partition length the device chose
     n_parts = (L + part - 1) // part
@@ -207,6 +313,9 @@ def main() -> int:
     t_app = [0.0 if fused else evs[i][0].elapsed_time(evs[i][1]) * 1e-3 for i in sampled]
     t_dec = [evs[i][dec_from].elapsed_time(evs[i][2]) * 1e-3 for i in sampled]
     t_cmb = [evs[i][2].elapsed_time(evs[i][3]) * 1e-3 for i in sampled]
+    p_step = [e[0].elapsed_time(e[3]) * 1e-3 for e in pass_evs]
+    p_dec = [e[dec_from].elapsed_time(e[2]) * 1e-3 for e in pass_evs]
+    p_cmb = [e[2].elapsed_time(e[3]) * 1e-3 for e in pass_evs]
     step_s = wall / args.steps  # whole-job rate over the timed region
     dec_s = sum(t_dec) / len(t_dec)
 
@@ -253,9 +362,13 @@ def main() -> int:
                       "decode": round(1e6 * dec_s, 2),
                       "combine": round(1e6 * sum(t_cmb) / len(t_cmb), 2),
                       "event_step": round(1e6 * sum(t_step) / len(t_step), 2),
-                      "decode_p10_p50_p90": _pcts(t_dec),
-                      "event_step_p10_p50_p90": _pcts(t_step),
-                      "sampled_steps": len(sampled), "sampled_every": args.event_every},
+                      "sampled_steps": len(sampled), "sampled_every": args.event_every,
+                      # percentiles: the event pass after the timed region
+                      "decode_p10_p50_p90": _pcts(p_dec),
+                      "combine_p10_p50_p90": _pcts(p_cmb),
+                      "event_step_p10_p50_p90": _pcts(p_step),
+                      "percentile_samples": n_pass},
+        "gpu_state": gpu_state,
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
         "roofline": {"bound": "hbm", "kernel": "rkv::decode_kernel<256, 1, false, 2, 1, false>",
@@ -272,19 +385,53 @@ def main() -> int:
         res["roofline"]["frac_of_stream_ceiling"] = round(res["roofline"]["achieved"] / best, 4)
         # the decode's own tile order over this pool's (shuffled) pages, with
         # nothing computed: the read rate that access pattern reaches here
-        pat = pattern_ceiling(rkv, ctx, pool, g, B, L, part, pages_per_seq, kv_bytes, stream)
-        res["pattern_read_ceiling"] = pat
-        # K/V bytes over the decode kernel's time against the same bytes over the pattern's
-        res["roofline"]["frac_of_pattern_ceiling"] = round(pat["us"] * 1e-6 / dec_s, 4)
+        if L % 32:
+            res["pattern_read_ceiling"] = {"skipped": f"ctx {L} is not a whole number of "
+                                                      "32-token tiles"}
+        else:
+            pat = pattern_ceiling(rkv, ctx, pool, g, B, L, part, pages_per_seq, kv_bytes, stream)
+            res["pattern_read_ceiling"] = pat
+            # K/V bytes over the decode kernel's time against the same bytes over the pattern's
+            res["roofline"]["frac_of_pattern_ceiling"] = round(pat["us"] * 1e-6 / dec_s, 4)
 
     # ---- CPU baseline: the reference path restated in C, timed on a sample -------
     if args.cpu_sample_seqs > 0:
         res["cpu_baseline"] = cpu_baseline(rkv, ctx, pool, g, q, out, k_new, v_new, B, L, Hq, Hkv,
                                            D, scale, step_bytes, args.cpu_sample_seqs)
-    print(json.dumps(res), flush=True)
     pool.close()
+
+    # ---- configs 2, 3 and 5 in the same run (driver-timed secondary lines) -------
+    if args.secondary:
+        res["secondary"] = secondary(args)
+    print(json.dumps(res), flush=True)
     ctx.close()
     return 0
+
+
+def secondary(args) -> dict:
+    """Configs 2, 3 (device-chosen partitions, and the reference's 128) and 5
+    at the headline's --steps/--warmup, each a compact record of its own
+    line (run_config): us per step, whole-step GB/s and fraction of 8 TB/s,
+    the decode kernel's events and roofline fraction."""
+    import copy
+    out = {}
+    for name, cfg, part in (("config2", 2, 0), ("config3", 3, 0), ("config3_128_partitions", 3, 2048),
+                            ("config5", 5, 0)):
+        a = copy.copy(args)
+        a.config, a.partition_tokens, a.graph = cfg, part, False
+        r = run_config(a, emit=False)
+        rf = r.get("roofline", {})
+        out[name] = {"us_per_step": r["us_per_step"], "gbs": r["value"],
+                     "frac_of_hbm_peak": round(r["value"] / HBM_PEAK_GBS, 4),
+                     "decode_us": rf.get("decode_us"), "decode_frac": rf.get("frac"),
+                     "decode_p10_p50_p90": r.get("decode_p10_p50_p90"),
+                     "partition_tokens": r["config"]["partition_tokens"],
+                     "partitions": r["config"]["partitions_total"],
+                     "algorithmic_bytes_per_step": r["algorithmic_bytes_per_step"]}
+        if "graph_us_per_step" in r:
+            out[name]["graph_us_per_step"] = r["graph_us_per_step"]
+        print(f"[bench] secondary {name}: {r['us_per_step']} us/step", file=sys.stderr, flush=True)
+    return out
 
 
 def _pcts(xs):
@@ -525,7 +672,8 @@ class _Decoder:
         return int(self.ws[:4 * (1 + 2 * batch)].view(torch.int32)[2::2].sum().item())
 
 
-def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extra, dtype=DT_INT8_QK):
+def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extra, dtype=DT_INT8_QK,
+          emit=True):
     value = step_bytes / step_s / 1e9
     res = {
         "metric": f"config {cfg}: paged Q8 decode HBM GB/s (% of 8 TB/s) + us/step",
@@ -546,10 +694,12 @@ def _line(args, cfg, workload, step_s, dec_s, step_bytes, dec_bytes, flops, extr
                            "traffic": None, "algorithmic_bytes_per_launch": dec_bytes,
                            "decode_us": round(dec_s * 1e6, 2)}
     res.update(extra)
-    print(json.dumps(res), flush=True)
+    if emit:
+        print(json.dumps(res), flush=True)
+    return res
 
 
-def _time_steps(args, stream, step, n_events=2):
+def _time_steps(args, stream, step, n_events=2, event_pass=False):
     import torch
     for i in range(args.warmup):
         step(i, None)
@@ -566,6 +716,21 @@ def _time_steps(args, stream, step, n_events=2):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
     dec = sum(e[0].elapsed_time(e[1]) for e in evs.values()) * 1e-3 / len(evs)
+    _time_steps.last_pcts = None
+    if not event_pass:
+        return wall, dec
+    # the event pass: every step with its events, for percentiles over at
+    # least 20 samples (after the timed region: markers cost the stream)
+    n_pass = max(getattr(args, "event_steps", 20), 20)
+    pev = [[torch.cuda.Event(enable_timing=True) for _ in range(n_events)] for _ in range(n_pass)]
+    for e in pev:
+        for x in e:
+            x.record(stream)
+    torch.cuda.synchronize()
+    for i, e in enumerate(pev):
+        step(args.warmup + args.steps + i, e)
+    torch.cuda.synchronize()
+    _time_steps.last_pcts = _pcts([e[0].elapsed_time(e[1]) * 1e-3 for e in pev])
     return wall, dec
 
 
@@ -593,7 +758,7 @@ def _time_graphs(args, dec, layers):
     return wall
 
 
-def run_config(args) -> int:
+def run_config(args, emit=True):
     """Configs 2, 3 and 5: every sequence keeps its length across steps (the
     appended rows overwrite the same slots), pools rotate over `layers` so the
     K/V stream does not fit the 256 MB Infinity Cache.  Config 5 also grows
@@ -669,7 +834,7 @@ def run_config(args) -> int:
                 pool.alloc.truncate(s, int(lens[s] + a[s]))
                 pool.alloc.truncate(s, int(lens[s]))  # steady state: drafts never commit
 
-    wall, dec_s = _time_steps(args, stream, step)
+    wall, dec_s = _time_steps(args, stream, step, event_pass=True)
     ctx.sync()
     launch = "eager"
     graph_wall = None
@@ -690,17 +855,18 @@ def run_config(args) -> int:
     step_bytes = kv + qo + bt + apb
     # causal draft rows: row j attends ctx+j+1 positions
     flops = 4 * D * Hq * sum(int(c) - q_len + j + 1 for c in cap for j in range(q_len))
-    _line(args, cfg, work, wall, dec_s, step_bytes, step_bytes, flops,
-          {"config": {"batch": B, "q_len": q_len, "layers_rotated": layers,
-                      "partition_tokens": pt, "partitions_total": n_parts,
-                      "pool_pages_per_layer": num_pages, "launch": launch},
-           **({"graph_us_per_step": round(graph_wall * 1e6, 2)} if graph_wall else {}),
-           "split_k_partial_bytes": n_parts * q_len * Hq * (D + 2) * 4,
-           **({"mean_accept": float(np.mean(accepts))} if accepts else {})},
-          dtype=DT_F16_QK if q_len * Hq // Hkv > 8 else DT_INT8_QK)
+    res = _line(args, cfg, work, wall, dec_s, step_bytes, step_bytes, flops,
+                {"config": {"batch": B, "q_len": q_len, "layers_rotated": layers,
+                            "partition_tokens": pt, "partitions_total": n_parts,
+                            "pool_pages_per_layer": num_pages, "launch": launch},
+                 **({"graph_us_per_step": round(graph_wall * 1e6, 2)} if graph_wall else {}),
+                 "split_k_partial_bytes": n_parts * q_len * Hq * (D + 2) * 4,
+                 "decode_p10_p50_p90": _time_steps.last_pcts,
+                 **({"mean_accept": float(np.mean(accepts))} if accepts else {})},
+                dtype=DT_F16_QK if q_len * Hq // Hkv > 8 else DT_INT8_QK, emit=emit)
     pool.close()
     ctx.close()
-    return 0
+    return res if not emit else 0
 
 
 def run_config4(args) -> int:

@@ -368,7 +368,8 @@ rkv_status rkv_flash_decode_q8(rkv_ctx *ctx, const rkv_flash_decode_params *p,
  * gather, spill, restore) run in call order, whatever streams they are
  * queued on: a call on another stream than the pool's previous call first
  * makes its stream wait, on the device, for the work queued so far on that
- * previous stream (which must still exist then).  Calls on one stream add
+ * previous stream (which must still exist then, unless it was released with
+ * rkv_pool_release_stream).  Calls on one stream add
  * nothing. */
 /* Where a pool's pages live.  RKV_PAGES_HOST puts them in pinned host
  * memory mapped for the device (the reference's host-KV tier,
@@ -393,6 +394,13 @@ typedef struct rkv_pool_desc {
 typedef struct rkv_pool rkv_pool;
 rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **out);
 rkv_status rkv_pool_destroy(rkv_pool *pool);
+/* The pool forgets `stream` if its previous call was queued there: the work
+ * queued on it so far is marked (an event recorded now), and the next call,
+ * on any stream, waits for that mark instead of touching `stream`.  Call it
+ * before destroying a stream the pool's last call used; other calls need
+ * nothing.  No reference counterpart (Vulkan queues outlive their
+ * submissions, har-vulkan/src/lib.rs:1673-1777). */
+rkv_status rkv_pool_release_stream(rkv_pool *pool, void *stream);
 rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
 /* Upload the allocator's changed block-table rows and all lengths and run
  * its queued copy-on-write page copies (all layers), ordered on `stream`:
@@ -414,6 +422,11 @@ rkv_status rkv_pool_decode(rkv_pool *pool, int32_t layer, const rkv_decode_args 
  * allocator's length of each sequence. */
 rkv_status rkv_pool_prefill(rkv_pool *pool, int32_t layer, const rkv_prefill_args *args,
                             void *stream);
+/* rkv_prefill_workspace_bytes for rkv_pool_prefill on this pool: a pool in
+ * host memory widens each tile in the row blocks that read it (its pages
+ * cross the host link once per row block either way), so it needs only the
+ * split partials, planned for its dispatch order. */
+size_t rkv_pool_prefill_workspace_bytes(const rkv_pool *pool, const rkv_prefill_args *args);
 rkv_status rkv_pool_gather(rkv_pool *pool, int32_t layer, int32_t seq, int32_t kind,
                            uint8_t *out, void *stream);
 
@@ -658,7 +671,9 @@ rkv_status rkv_stream_read(rkv_ctx *ctx, const void *data, uint64_t bytes, int32
  * codes, V codes and both scale runs, with the decode's nontemporal 1 KiB
  * LDS-DMA copies and one tile in flight.  Nothing is written.  head_dim 128
  * or 256, page_tokens >= 32; seq_tokens a multiple of 32; partition_tokens a
- * multiple of page_tokens of at most 64 pages; the rows must hold
+ * multiple of 32 (partitions start on 32-token tiles, inside a page when it
+ * is not a whole number of pages, as the decode's do) whose every partition
+ * spans at most 64 pages; the rows must hold
  * ceil(seq_tokens / page_tokens) pages (a page id outside the pool reads
  * page 0).  Reads n_seqs * kv_heads * seq_tokens * head_dim * 17/8 bytes.
  * Stream-ordered. */

@@ -163,6 +163,7 @@ _SIGS = {
                                           C.POINTER(DecodeArgs), P]),
     "rkv_decode_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
     "rkv_prefill_workspace_bytes": (C.c_size_t, [C.POINTER(Geometry), C.POINTER(PrefillArgs)]),
+    "rkv_pool_prefill_workspace_bytes": (C.c_size_t, [P, C.POINTER(PrefillArgs)]),
     "rkv_decode_partition_tokens": (C.c_int32, [C.POINTER(Geometry), C.POINTER(DecodeArgs)]),
     "rkv_decode_q8_partials": (C.c_int32, [P, C.POINTER(Geometry), P, P, C.c_int32, P,
                                            C.c_int32, C.POINTER(DecodeArgs), P, P, P]),
@@ -175,6 +176,7 @@ _SIGS = {
     "rkv_flash_decode_q8": (C.c_int32, [P, C.POINTER(FlashDecodeParams), P, P, P, P, P, P]),
     "rkv_pool_create": (C.c_int32, [P, C.POINTER(PoolDesc), C.POINTER(P)]),
     "rkv_pool_destroy": (C.c_int32, [P]),
+    "rkv_pool_release_stream": (C.c_int32, [P, P]),
     "rkv_pool_allocator": (P, [P]),
     "rkv_pool_sync_tables": (C.c_int32, [P, P]),
     "rkv_pool_layer_pages": (P, [P, C.c_int32]),
@@ -638,6 +640,10 @@ class Pool:
     def sync_tables(self, stream=None) -> None:
         check(lib().rkv_pool_sync_tables(self.h, _stream(stream)))
 
+    def release_stream(self, stream) -> None:
+        """Let the pool forget `stream` (before the caller destroys it)."""
+        check(lib().rkv_pool_release_stream(self.h, _stream(stream)))
+
     def layer_pages(self, layer: int) -> int:
         return lib().rkv_pool_layer_pages(self.h, layer)
 
@@ -660,6 +666,9 @@ class Pool:
 
     def prefill(self, layer, a: PrefillArgs, stream=None) -> None:
         check(lib().rkv_pool_prefill(self.h, layer, C.byref(a), _stream(stream)))
+
+    def prefill_workspace_bytes(self, a: PrefillArgs) -> int:
+        return lib().rkv_pool_prefill_workspace_bytes(self.h, C.byref(a))
 
     def r4kv_page_bytes(self, token_count, layer_lo, layer_hi) -> int:
         return lib().rkv_r4kv_page_bytes(self.h, token_count, layer_lo, layer_hi)
@@ -782,6 +791,10 @@ class Serve:
 
     def sync_tables(self, stream=None) -> None:
         check(lib().rkv_pool_sync_tables(self.pool_h, _stream(stream)))
+
+    def release_stream(self, stream) -> None:
+        """Let the adapter's pool forget `stream` (before the caller destroys it)."""
+        check(lib().rkv_pool_release_stream(self.pool_h, _stream(stream)))
 
     def page_location(self, sid: int, ordinal: int) -> PageLocation:
         loc = PageLocation()

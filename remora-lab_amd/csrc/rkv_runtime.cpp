@@ -123,12 +123,12 @@ rkv_status rkv_ctx_create(int32_t device, rkv_ctx **out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return fail(RKV_ERR_UNSUPPORTED, op, "device %d is %s; kernels are built for gfx950", device,
                 prop.gcnArchName);
-  // the decode's partition plan and the prefill's dispatch simulation are
-  // sized for the whole chip: 256 CUs in 8 XCDs
-  if (prop.multiProcessorCount != rkv::kComputeUnits)
-    return fail(RKV_ERR_UNSUPPORTED, op,
-                "device %d has %d compute units; the launch plans are sized for %d (a whole "
-                "MI355X, 8 XCDs)", device, prop.multiProcessorCount, rkv::kComputeUnits);
+  // The decode's partition plan, the prefill's dispatch simulation and the
+  // workspace sizes that follow from them are sized for the whole chip (256
+  // CUs in 8 XCDs) whatever the device reports: a part with fewer CUs (a
+  // partition mode) runs the same launches in more rounds, correct and
+  // slower.  The workspace queries take no context, so the plans cannot
+  // follow the device.
   // the static decode scratch of rkv_decode_q8_noalloc, resolved once per
   // device with the device current
   void *scratch = nullptr;
@@ -978,7 +978,14 @@ rkv_status rkv_prefill_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, const void *pa
                     rkv::kPrefillXcdChunkHbm);
 }
 
-size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_args *a) {
+}  // extern "C"
+
+namespace {
+// Workspace of a prefill launched with this XCD chunk (the split plan's
+// dispatch simulation depends on it), with room for the widened tiles when
+// the launch would widen once (HBM pages and a bf16 query).
+size_t prefill_ws_query(const rkv_kv_geometry *g, const rkv_prefill_args *a, int32_t xcd_chunk,
+                        bool widen_once) {
   if (!g || !a || check_geometry(g, "rkv_prefill_workspace_bytes") != RKV_OK) return 0;
   if (a->n_seqs < 1 || a->n_seqs > RKV_PREFILL_MAX_SEQS || !a->ctx_lens || !a->q_rows) return 0;
   if (a->q_heads < 1 || a->q_heads % g->kv_heads != 0) return 0;
@@ -987,10 +994,17 @@ size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_a
   for (int32_t e = 0; e < a->n_seqs; ++e)
     if (a->ctx_lens[e] < 0 || a->q_rows[e] < 0) return 0;
   const SegPlan sp = plan_segments(g, a->q_heads, rkv::kPrefillRows / G, a->n_seqs, a->ctx_lens,
-                                   a->q_rows, a->segment_tokens, SIZE_MAX, rkv::kPrefillXcdChunkHbm);
+                                   a->q_rows, a->segment_tokens, SIZE_MAX, xcd_chunk);
   const size_t partials = prefill_ws_bytes(sp.partial_rows, g->head_dim);
-  if (a->q_dtype != RKV_BF16) return partials;
+  if (a->q_dtype != RKV_BF16 || !widen_once) return partials;
   return prefill_pre_at(partials) + prefill_pre_bytes(g, a->n_seqs, a->ctx_lens, a->q_rows);
+}
+}  // namespace
+
+extern "C" {
+
+size_t rkv_prefill_workspace_bytes(const rkv_kv_geometry *g, const rkv_prefill_args *a) {
+  return prefill_ws_query(g, a, rkv::kPrefillXcdChunkHbm, true);
 }
 
 rkv_status rkv_append_q8(rkv_ctx *ctx, const rkv_kv_geometry *g, void *pages,
@@ -1350,6 +1364,10 @@ struct rkv_pool {
   // the stream of the pool's last call (see order_after_last)
   hipStream_t last_stream = nullptr;
   bool has_last = false;
+  // rkv_pool_release_stream forgot last_stream: `handoff` already marks the
+  // work queued on it (when handoff_set; a capturing stream has none)
+  bool released = false;
+  bool handoff_set = false;
   hipEvent_t handoff = nullptr;
 };
 
@@ -1368,8 +1386,17 @@ size_t stage_ints(const rkv_pool_desc &d) {
 // stream is left alone: a capturing stream may neither wait on nor record for
 // work outside its capture, and the stream the graph is launched on orders the
 // captured calls when it runs.
+// A stream the caller released (rkv_pool_release_stream) is never touched
+// again: its handoff event was recorded at the release.
 rkv_status order_after_last(rkv_pool *p, hipStream_t hs, const char *op) {
-  if (p->has_last && p->last_stream != hs) {
+  if (p->released) {
+    hipStreamCaptureStatus now = hipStreamCaptureStatusNone;
+    hipError_t e;
+    if ((e = hipStreamIsCapturing(hs, &now)) != hipSuccess) return hip_fail(op, e);
+    if (p->handoff_set && now == hipStreamCaptureStatusNone &&
+        (e = hipStreamWaitEvent(hs, p->handoff, 0)) != hipSuccess)
+      return hip_fail(op, e);
+  } else if (p->has_last && p->last_stream != hs) {
     hipStreamCaptureStatus now = hipStreamCaptureStatusNone, before = hipStreamCaptureStatusNone;
     hipError_t e;
     if ((e = hipStreamIsCapturing(hs, &now)) != hipSuccess ||
@@ -1382,6 +1409,7 @@ rkv_status order_after_last(rkv_pool *p, hipStream_t hs, const char *op) {
   }
   p->last_stream = hs;
   p->has_last = true;
+  p->released = false;
   return RKV_OK;
 }
 }  // namespace
@@ -1483,6 +1511,23 @@ rkv_status rkv_pool_destroy(rkv_pool *p) {
   if (p->handoff) (void)hipEventDestroy(p->handoff);
   rkv_alloc_destroy(p->alloc);
   delete p;
+  return RKV_OK;
+}
+
+rkv_status rkv_pool_release_stream(rkv_pool *pool, void *stream) {
+  const char *op = "rkv_pool_release_stream";
+  if (!pool) return fail(RKV_ERR_INVALID_ARG, op, "pool is NULL");
+  if (rkv_status s = use_device(pool->ctx, op)) return s;
+  hipStream_t hs = as_stream(stream);
+  if (pool->released || !pool->has_last || pool->last_stream != hs) return RKV_OK;
+  hipStreamCaptureStatus now = hipStreamCaptureStatusNone;
+  hipError_t e;
+  if ((e = hipStreamIsCapturing(hs, &now)) != hipSuccess) return hip_fail(op, e);
+  // a capturing stream's calls are ordered by the stream its graph runs on
+  pool->handoff_set = now == hipStreamCaptureStatusNone;
+  if (pool->handoff_set && (e = hipEventRecord(pool->handoff, hs)) != hipSuccess)
+    return hip_fail(op, e);
+  pool->released = true;
   return RKV_OK;
 }
 
@@ -1590,6 +1635,13 @@ rkv_status rkv_pool_prefill(rkv_pool *p, int32_t layer, const rkv_prefill_args *
   return prefill_q8(p->ctx, &p->g, rkv_pool_layer_pages(p, layer), p->d_tables,
                     p->d.max_pages_per_seq, p->d.max_seqs, args, stream,
                     host ? rkv::kPrefillXcdChunkHost : rkv::kPrefillXcdChunkHbm, !host);
+}
+
+size_t rkv_pool_prefill_workspace_bytes(const rkv_pool *p, const rkv_prefill_args *args) {
+  if (!p) return 0;
+  const bool host = p->d.page_memory == RKV_PAGES_HOST;
+  return prefill_ws_query(&p->g, args, host ? rkv::kPrefillXcdChunkHost : rkv::kPrefillXcdChunkHbm,
+                          !host);
 }
 
 rkv_status rkv_pool_gather(rkv_pool *p, int32_t layer, int32_t seq, int32_t kind, uint8_t *out,
@@ -1701,10 +1753,18 @@ rkv_status rkv_stream_read_tiles(rkv_ctx *ctx, const rkv_kv_geometry *g, const v
   if (!pages || !block_tables) return fail(RKV_ERR_INVALID_ARG, op, "NULL pages/block_tables");
   if (n_seqs < 1 || seq_tokens < 32 || seq_tokens % 32 != 0)
     return fail(RKV_ERR_INVALID_ARG, op, "n_seqs=%d seq_tokens=%d", n_seqs, seq_tokens);
-  if (partition_tokens < g->page_tokens || partition_tokens % g->page_tokens != 0 ||
-      partition_tokens / g->page_tokens > 64)
-    return fail(RKV_ERR_INVALID_ARG, op, "partition_tokens=%d (page_tokens %d, at most 64 pages)",
-                partition_tokens, g->page_tokens);
+  if (partition_tokens < 32 || partition_tokens % 32 != 0)
+    return fail(RKV_ERR_INVALID_ARG, op, "partition_tokens=%d (a multiple of 32)", partition_tokens);
+  // partitions start on 32-token tiles, inside a page when partition_tokens
+  // is not a whole number of pages; each must span at most 64 pages (the
+  // kernel holds one page id per lane), the decode's rule
+  for (int64_t t0 = 0; t0 < seq_tokens; t0 += partition_tokens) {
+    const int64_t t1 = std::min<int64_t>(seq_tokens, t0 + partition_tokens);
+    if ((t1 - 1) / g->page_tokens - t0 / g->page_tokens + 1 > 64)
+      return fail(RKV_ERR_INVALID_ARG, op,
+                  "partition_tokens=%d: the partition at token %lld spans more than 64 pages of %d",
+                  partition_tokens, (long long)t0, g->page_tokens);
+  }
   if ((seq_tokens + g->page_tokens - 1) / g->page_tokens > bt_stride)
     return fail(RKV_ERR_INVALID_ARG, op, "seq_tokens=%d needs more pages than bt_stride=%d",
                 seq_tokens, bt_stride);

@@ -89,11 +89,13 @@ __global__ __launch_bounds__(64) void stream_tiles_kernel(TileStreamLaunch t) {
   const int lane = threadIdx.x;
   const int kvh = blockIdx.y;
   const int b = blockIdx.x / t.parts, part = blockIdx.x % t.parts;
+  // a partition starts on a 32-token tile, possibly inside a page; the host
+  // checked that every partition spans at most 64 pages
   const int32_t tok0 = part * t.part_tokens;
   const int32_t tok_end = min(t.seq_tokens, tok0 + t.part_tokens);
   const int n_tiles = (tok_end - tok0) / 32;
   const int pg0 = tok0 / g.page_tokens;
-  const int npg = (tok_end - tok0 + g.page_tokens - 1) / g.page_tokens;
+  const int npg = (tok_end - 1) / g.page_tokens - pg0 + 1;
   int32_t pid = lane < npg ? t.bt[(int64_t)b * t.bt_stride + pg0 + lane] : 0;
   if (pid < 0 || pid >= g.num_pages) pid = 0;  // every copy stays inside the pool
   const uint64_t RB = region_bytes(g), PB = page_bytes(g);
@@ -103,8 +105,9 @@ __global__ __launch_bounds__(64) void stream_tiles_kernel(TileStreamLaunch t) {
   const uint32_t sc_off = lane < D / 8 ? PTD + 16u * lane
                                        : (lane < D / 4 ? (uint32_t)RB + PTD + 16u * (lane - D / 8) : PTD);
   for (int i = 0; i < n_tiles; ++i) {
-    const int32_t s0 = (i * 32) % g.page_tokens;
-    const int32_t p = __builtin_amdgcn_readlane(pid, (i * 32) / g.page_tokens);
+    const int32_t tk = tok0 + i * 32;
+    const int32_t s0 = tk % g.page_tokens;
+    const int32_t p = __builtin_amdgcn_readlane(pid, tk / g.page_tokens - pg0);
     const uint8_t *kb = t.pages + (uint64_t)p * PB + (uint64_t)(2 * kvh) * RB;
     uint8_t *dst = st[i & 1];
 #pragma unroll

@@ -103,6 +103,31 @@ def test_host_pool_matches_device_pool(rkv, rko, ctx, Hq, Hkv, D, PT, lens):
             want = _attend(rko, kbytes[b], vbytes[b], Hq, Hkv, D, L - k + j + 1, qp[off + j], scale)
             assert_close(outs[1][off + j].reshape(-1), want, what=f"host pool prefill seq {b} row {j}")
         off += k
+    # a bf16 query with the workspace each pool asks for: the HBM pool's also
+    # holds every tile widened once, the host pool's only the split partials
+    qb = qpd.to(torch.bfloat16)
+    qb_h = qb.float().cpu().numpy()
+    cols = (list(range(B)), [L - k for L, k in zip(lens, n)], n)
+    need = [pool.prefill_workspace_bytes(rkv.prefill_args(*cols, qb, torch.zeros_like(qpd), scale))
+            for pool in pools]
+    partials = [pool.prefill_workspace_bytes(rkv.prefill_args(*cols, qpd, torch.zeros_like(qpd),
+                                                              scale)) for pool in pools]
+    assert need[0] > partials[0] and need[1] == partials[1], (need, partials)
+    outs = []
+    for pool, nb in zip(pools, need):
+        o = torch.empty(qp.shape, dtype=torch.float32, device="cuda")
+        ws = torch.empty(max(nb, 1), dtype=torch.uint8, device="cuda")
+        pool.prefill(0, rkv.prefill_args(*cols, qb, o, scale, workspace=ws))
+        ctx.sync()
+        outs.append(o.cpu().numpy())
+    assert_close(outs[1], outs[0], what="bf16 q prefill: host pool vs HBM pool")
+    off = 0
+    for b, (L, k) in enumerate(zip(lens, n)):
+        for j in (0, k - 1):
+            want = _attend(rko, kbytes[b], vbytes[b], Hq, Hkv, D, L - k + j + 1, qb_h[off + j], scale)
+            assert_close(outs[1][off + j].reshape(-1), want,
+                         what=f"host pool bf16 q prefill seq {b} row {j}")
+        off += k
     for pool in pools:
         pool.close()
 

@@ -265,3 +265,63 @@ def test_serve_steps_alternate_streams(rkv, rko, ctx):
             want = m.attend(sid, 0, ctx_len + step + 1, qd[step][b], scale)
             assert_close(got[b].reshape(-1), want, what=f"step {step} id {sid}")
     sv.close()
+
+
+def test_serve_steps_on_released_streams(rkv, rko, ctx):
+    """Every step on a stream of its own that the caller releases from the
+    pool (rkv_pool_release_stream) and destroys right after queueing the
+    step, with no host synchronization: the next step's calls wait for the
+    released stream's work through the mark the release recorded, never
+    touching the destroyed handle, and every decode row matches the oracle."""
+    import ctypes
+    import os
+    torch = __import__("torch")
+    # the HIP runtime torch loaded (the one librkv.so is bound to)
+    hip = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD)
+    D, Hkv, Hq, PT, ctx_len, n_seq, steps = 128, 2, 16, 32, 700, 3, 5
+    scale = 1.0 / math.sqrt(D)
+    sv = rkv.Serve(ctx, 1, Hkv, D, PT, num_pages=n_seq * (ctx_len // PT + 3) + 8, max_seqs=n_seq,
+                   max_pages_per_seq=ctx_len // PT + 3, q_heads=Hq, max_decode=n_seq,
+                   max_prefill_rows=n_seq * ctx_len, seed=4)
+    m = _Model(rko, 1, Hkv, Hq, D)
+    rng = np.random.default_rng(12)
+    ids = list(range(31, 31 + n_seq))
+    for sid in ids:
+        m.admit(sid)
+    n_pf = n_seq * ctx_len
+    kp = rng.standard_normal((n_pf, Hkv, D)).astype(np.float32)
+    vp = rng.standard_normal((n_pf, Hkv, D)).astype(np.float32)
+    qp = rng.standard_normal((n_pf, Hq, D)).astype(np.float32)
+    op = torch.empty((n_pf, Hq, D), dtype=torch.float32, device="cuda")
+    sv.begin_step(prefill=[(sid, ctx_len) for sid in ids], decode=[])
+    sv.prefill(0, torch.from_numpy(qp).cuda(), torch.from_numpy(kp).cuda(),
+               torch.from_numpy(vp).cuda(), op, scale)
+    ctx.sync()
+    for i, sid in enumerate(ids):
+        m.append(sid, 0, kp[i * ctx_len:(i + 1) * ctx_len], vp[i * ctx_len:(i + 1) * ctx_len])
+    qd = [rng.standard_normal((n_seq, Hq, D)).astype(np.float32) for _ in range(steps)]
+    kd = [rng.standard_normal((n_seq, Hkv, D)).astype(np.float32) for _ in range(steps)]
+    vd = [rng.standard_normal((n_seq, Hkv, D)).astype(np.float32) for _ in range(steps)]
+    dq = [torch.from_numpy(x).cuda() for x in qd]
+    dk = [torch.from_numpy(x).cuda() for x in kd]
+    dv = [torch.from_numpy(x).cuda() for x in vd]
+    od = [torch.zeros((n_seq, Hq, D), dtype=torch.float32, device="cuda") for _ in range(steps)]
+    torch.cuda.synchronize()
+    print(f"serve: {steps} decode steps, each on a stream released and destroyed after it",
+          flush=True)
+    for step in range(steps):
+        st = ctypes.c_void_p()
+        assert hip.hipStreamCreate(ctypes.byref(st)) == 0
+        sv.begin_step(prefill=[], decode=[(sid, 1) for sid in ids], stream=st.value)
+        sv.decode(0, dq[step], dk[step], dv[step], od[step], scale, stream=st.value)
+        sv.release_stream(st.value)
+        assert hip.hipStreamDestroy(st) == 0
+    torch.cuda.synchronize()
+    ctx.sync()
+    for step in range(steps):
+        got = od[step].cpu().numpy()
+        for b, sid in enumerate(ids):
+            m.append(sid, 0, kd[step][b:b + 1], vd[step][b:b + 1])
+            want = m.attend(sid, 0, ctx_len + step + 1, qd[step][b], scale)
+            assert_close(got[b].reshape(-1), want, what=f"step {step} id {sid}")
+    sv.close()

@@ -54,11 +54,23 @@ def test_tile_order_read_runs_and_bad_args_are_refused(rkv, ctx):
         bt[1, 3] = num_pages + 7  # outside the pool: read as page 0
         before = pages.clone()
         rkv.stream_read_tiles(ctx, g, pages, bt, npg, B, L, min(64 * PT, 1024))
+        # partitions of whole tiles that start inside pages (the decode's
+        # lengths in 32-token steps): 96 tokens, and 63 pages plus a tile
+        for part in (96, 63 * PT + 32):
+            if part < L and part % PT:
+                rkv.stream_read_tiles(ctx, g, pages, bt, npg, B, L, part)
         ctx.sync()
         assert torch.equal(pages, before)
+    # refusals, on 32-token pages (128 per sequence)
+    PT = 32
+    npg = L // PT
+    g = rkv.geometry(Hkv, 128, PT, B * npg + 5)
+    pages = torch.zeros(g.num_pages * rkv.page_bytes(g), dtype=torch.uint8, device="cuda")
+    bt = torch.from_numpy(np.arange(B * npg, dtype=np.int32).reshape(B, npg)).cuda()
+    rkv.stream_read_tiles(ctx, g, pages, bt, npg, B, L, 64 * PT)  # 64 pages: accepted
     for bt_stride, n, L, part in [(npg, B, L + 16, 1024),   # not a multiple of 32
-                                  (npg, B, L, 48),          # not a multiple of page_tokens
-                                  (npg, B, L, 64 * PT * 2),  # more than 64 pages
+                                  (npg, B, L, 48),          # not a multiple of 32
+                                  (npg, B, L, 64 * PT + 32),  # the first partition spans 65 pages
                                   (npg - 1, B, L, 1024),     # rows too short
                                   (npg, 0, L, 1024)]:        # no sequences
         with pytest.raises(rkv.RkvError):
