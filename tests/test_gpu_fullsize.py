@@ -222,9 +222,10 @@ def test_fullsize_config2(rkv, rko, ctx):
 @pytest.mark.parametrize("partition_tokens", [0, 2048])
 def test_fullsize_config3(rkv, rko, ctx, partition_tokens):
     """Config 3: one sequence of 262,144 tokens (the last appended by the
-    decode launch), Hq 16 / Hkv 2, D 256: device-chosen partitions (512, with
-    the two-level combine) and the reference's 128 partitions of 2048 tokens;
-    all 16 heads checked, for an N(0,1) query and one with outlier channels."""
+    decode launch), Hq 16 / Hkv 2, D 256: device-chosen partitions (482 of 544
+    tokens at this length, merged by the one-launch combine) and the
+    reference's 128 partitions of 2048 tokens; all 16 heads checked, for an
+    N(0,1) query and one with outlier channels."""
     torch = _torch()
     L = 262144
     print(f"config3 L={L} partition_tokens={partition_tokens}", flush=True)

@@ -376,3 +376,28 @@ def test_har_kv_geometry_bytes(rko, kat):
     lay = rko.layout(4, 256, 64, g["tokens"] // 64)
     assert rko.page_bytes(lay) // 64 // 2 == g["q8_row_bytes"]  # per token, K or V
     assert rko.page_bytes(lay) * (g["tokens"] // 64) * 16 == g["total_bytes"]
+
+
+def _lcg_state(seed: int, n: int) -> int:
+    """State of q4k.rs:109-120's LCG after n steps, in closed form (the
+    skip-ahead of an affine recurrence): s_n = a^n s_0 + c (a^n - 1)/(a - 1)
+    mod 2^64.  (a - 1) is even, so the geometric sum is taken exactly from
+    a^n mod 2^64 (a - 1) instead of by a modular inverse."""
+    a, c, m = 6364136223846793005, 1442695040888963407, 1 << 64
+    an = pow(a, n, m * (a - 1))
+    geo = (an - 1) // (a - 1)
+    return (an % m * seed + c * geo) % m
+
+
+@pytest.mark.parametrize("seed", [0, 1, 3000, 1000 + (3 * 1024 + 1023) * 31, 2**64 - 1])
+def test_lcg_values_closed_form(rko, seed):
+    """rko_lcg_values (the smoke's K/V and query generator) against the
+    LCG's closed-form state at sampled indices up to 10^6: value i is
+    ((s_{i+1} >> 40) / 2^24) - 0.5, exact in f32."""
+    n = 1_000_000 if seed in (0, 3000) else 4096
+    got = rko.lcg_values(n, seed)
+    for i in sorted({0, 1, 2, 17, 1023, n // 3, n - 2, n - 1}):
+        s = _lcg_state(seed, i + 1)
+        want = np.float32(np.float32(s >> 40) / np.float32(1 << 24)) - np.float32(0.5)
+        assert got[i] == want, (seed, i, float(got[i]), float(want))
+    assert np.all(got >= -0.5) and np.all(got < 0.5)
