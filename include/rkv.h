@@ -405,9 +405,12 @@ rkv_alloc *rkv_pool_allocator(rkv_pool *pool);
 /* Upload the allocator's changed block-table rows and all lengths and run
  * its queued copy-on-write page copies (all layers), ordered on `stream`:
  * launches enqueued on `stream` afterwards see the new tables and copied
- * pages, earlier ones the old.  One pinned-staging copy plus one or two
- * small kernels; the host waits only if the staging buffer of the call
- * before last is still in flight. */
+ * pages, earlier ones the old.  One or two small kernels that read the
+ * changes from a pinned staging buffer in place (no copy and no event in
+ * the stream); the host waits only if the staging buffer of the call before
+ * last has not been read yet.  Refused (RKV_ERR_INVALID_ARG) on a stream
+ * that is capturing a graph: the upload carries the allocator's state at
+ * the call, which a replay would repeat. */
 rkv_status rkv_pool_sync_tables(rkv_pool *pool, void *stream);
 /* Device pointers owned by the pool (for a host-memory pool, the device
  * mapping of its pinned pages). */

@@ -315,18 +315,37 @@ namespace {
 // Unpack a block-table update: `n_rows` records of [seq][W page ids] then
 // the lengths of all `n_seqs` sequences.  Block i < n_rows copies record i;
 // block n_rows copies the lengths.
+// `packed` is the host's pinned staging buffer, read over the host link
+// (no separate copy).  When every block has read it, the last one to finish
+// stores `seq` to the host-visible word `done`, which tells the host that
+// the buffer may be rewritten: each block counts itself in the device
+// counter `count` (never reset; the launch's blocks are the counts from
+// `last` - gridDim.x + 1 to `last`).
 __global__ __launch_bounds__(256) void table_scatter_kernel(const int32_t *packed, int32_t n_rows,
                                                            int32_t W, int32_t n_seqs,
-                                                           int32_t *tables, int32_t *lens) {
+                                                           int32_t *tables, int32_t *lens,
+                                                           unsigned long long *count,
+                                                           unsigned long long last,
+                                                           unsigned long long *done,
+                                                           unsigned long long seq) {
   const int32_t r = blockIdx.x;
   if (r < n_rows) {
     const int32_t *rec = packed + (int64_t)r * (W + 1);
-    const int32_t seq = rec[0];
-    if (seq < 0 || seq >= n_seqs) return;  // packed by the host from its own table
-    for (int32_t i = threadIdx.x; i < W; i += 256) tables[(int64_t)seq * W + i] = rec[1 + i];
+    const int32_t sq = rec[0];
+    if (sq >= 0 && sq < n_seqs)  // packed by the host from its own table
+      for (int32_t i = threadIdx.x; i < W; i += 256) tables[(int64_t)sq * W + i] = rec[1 + i];
   } else {
     const int32_t *src = packed + (int64_t)n_rows * (W + 1);
     for (int32_t i = threadIdx.x; i < n_seqs; i += 256) lens[i] = src[i];
+  }
+  // every value read above was stored, so the block's reads are done
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __threadfence();
+    if (atomicAdd(count, 1ull) == last) {
+      __threadfence_system();
+      __hip_atomic_store(done, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
   }
 }
 
@@ -380,9 +399,11 @@ hipError_t launch_copy_pages(uint8_t *pages, int64_t layer_stride, int32_t layer
 }
 
 hipError_t launch_table_scatter(const int32_t *packed, int32_t n_rows, int32_t W, int32_t n_seqs,
-                                int32_t *tables, int32_t *lens, hipStream_t s) {
+                                int32_t *tables, int32_t *lens, unsigned long long *count,
+                                unsigned long long last, unsigned long long *done,
+                                unsigned long long seq, hipStream_t s) {
   hipLaunchKernelGGL(table_scatter_kernel, dim3((unsigned)n_rows + 1), dim3(256), 0, s, packed,
-                     n_rows, W, n_seqs, tables, lens);
+                     n_rows, W, n_seqs, tables, lens, count, last, done, seq);
   return hipGetLastError();
 }
 

@@ -33,9 +33,14 @@ hipError_t launch_import(const Geo &g, uint8_t *pages, const int32_t *bt, int32_
                          int32_t kind, const uint8_t *rows, int32_t *fault, hipStream_t s);
 hipError_t launch_f32_to_f16(const float *in, uint16_t *out, int64_t n, int32_t rule,
                              hipStream_t s);
-// block-table update: records [seq][W ids] x n_rows, then n_seqs lengths
+// block-table update: records [seq][W ids] x n_rows, then n_seqs lengths,
+// read from `packed` (pinned host memory, device-mapped); n_rows + 1 blocks,
+// each counted once in *count, and the block that takes the count `last`
+// stores `seq` to *done (host-visible) after every block has read `packed`
 hipError_t launch_table_scatter(const int32_t *packed, int32_t n_rows, int32_t W, int32_t n_seqs,
-                                int32_t *tables, int32_t *lens, hipStream_t s);
+                                int32_t *tables, int32_t *lens, unsigned long long *count,
+                                unsigned long long last, unsigned long long *done,
+                                unsigned long long seq, hipStream_t s);
 // copy-on-write: page dst := page src for each (src, dst) pair in `pairs`
 // (device), in `layers` page arrays `layer_stride` bytes apart
 hipError_t launch_copy_pages(uint8_t *pages, int64_t layer_stride, int32_t layers,

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -12,6 +13,7 @@
 #include <cstring>
 #include <functional>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/rkv.h"
@@ -1354,9 +1356,18 @@ struct rkv_pool {
   // other sync, after the event recorded behind the last kernel that read its
   // device buffer, so syncs on different streams never overwrite a buffer
   // still in use.
+  // table-sync staging: two pinned, coherent host buffers that the scatter
+  // kernel reads in place (their device mappings d_stage), alternately; the
+  // kernel's last block stores the sync's number to done[slot] (pinned,
+  // coherent) once every block has read the buffer, and a sync waits for
+  // that before it rewrites the slot.  scatter_count is the device counter
+  // of the scatter blocks run so far, scatter_blocks the blocks launched.
   int32_t *h_stage[2] = {nullptr, nullptr};
-  hipEvent_t stage_done[2] = {nullptr, nullptr};
   int32_t *d_stage[2] = {nullptr, nullptr};
+  unsigned long long *done = nullptr, *d_done = nullptr;
+  unsigned long long slot_sync[2] = {0, 0};  // the sync that last used each slot (0: none)
+  unsigned long long *scatter_count = nullptr;
+  unsigned long long scatter_blocks = 0;
   uint32_t n_syncs = 0;
   // R4KV page CRC: device result word and its pinned host copy
   uint32_t *d_crc = nullptr;
@@ -1386,6 +1397,26 @@ size_t stage_ints(const rkv_pool_desc &d) {
 // stream is left alone: a capturing stream may neither wait on nor record for
 // work outside its capture, and the stream the graph is launched on orders the
 // captured calls when it runs.
+// Wait until the scatter kernel of the sync that last used staging slot
+// `slot` has read it (its completion word reached that sync's number).
+// The wait spins on host memory; after two seconds it waits for the whole
+// device once, and a word still short then (the kernel did not run: a
+// device error) returns false instead of waiting on.
+bool wait_stage(rkv_pool *p, int slot) {
+  if (!p->done) return true;
+  const unsigned long long want = p->slot_sync[slot];
+  auto ready = [&] { return __atomic_load_n(&p->done[slot], __ATOMIC_ACQUIRE) >= want; };
+  const auto t0 = std::chrono::steady_clock::now();
+  while (!ready()) {
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::seconds(2)) {
+      (void)hipDeviceSynchronize();
+      return ready();
+    }
+    std::this_thread::yield();
+  }
+  return true;
+}
+
 // A stream the caller released (rkv_pool_release_stream) is never touched
 // again: its handoff event was recorded at the release.
 rkv_status order_after_last(rkv_pool *p, hipStream_t hs, const char *op) {
@@ -1459,12 +1490,19 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
        (e = hipMalloc(&p->pages, all_pages)) != hipSuccess) ||
       (e = hipMalloc(&p->d_tables, tbytes)) != hipSuccess ||
       (e = hipMalloc(&p->d_lens, sizeof(int32_t) * desc->max_seqs)) != hipSuccess ||
-      (e = hipMalloc(&p->d_stage[0], sbytes)) != hipSuccess ||
-      (e = hipMalloc(&p->d_stage[1], sbytes)) != hipSuccess ||
-      (e = hipHostMalloc(&p->h_stage[0], sbytes, hipHostMallocDefault)) != hipSuccess ||
-      (e = hipHostMalloc(&p->h_stage[1], sbytes, hipHostMallocDefault)) != hipSuccess ||
-      (e = hipEventCreateWithFlags(&p->stage_done[0], hipEventDisableTiming)) != hipSuccess ||
-      (e = hipEventCreateWithFlags(&p->stage_done[1], hipEventDisableTiming)) != hipSuccess ||
+      (e = hipHostMalloc(&p->h_stage[0], sbytes, hipHostMallocMapped | hipHostMallocCoherent)) !=
+          hipSuccess ||
+      (e = hipHostMalloc(&p->h_stage[1], sbytes, hipHostMallocMapped | hipHostMallocCoherent)) !=
+          hipSuccess ||
+      (e = hipHostGetDevicePointer(reinterpret_cast<void **>(&p->d_stage[0]), p->h_stage[0], 0)) !=
+          hipSuccess ||
+      (e = hipHostGetDevicePointer(reinterpret_cast<void **>(&p->d_stage[1]), p->h_stage[1], 0)) !=
+          hipSuccess ||
+      (e = hipHostMalloc(&p->done, 2 * sizeof(unsigned long long),
+                         hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess ||
+      (e = hipHostGetDevicePointer(reinterpret_cast<void **>(&p->d_done), p->done, 0)) != hipSuccess ||
+      (e = hipMalloc(&p->scatter_count, sizeof(unsigned long long))) != hipSuccess ||
+      (e = hipMemset(p->scatter_count, 0, sizeof(unsigned long long))) != hipSuccess ||
       (e = hipEventCreateWithFlags(&p->handoff, hipEventDisableTiming)) != hipSuccess ||
       (e = hipMalloc(&p->d_crc, 256)) != hipSuccess ||
       (e = hipHostMalloc(&p->h_crc, 256, hipHostMallocDefault)) != hipSuccess) {
@@ -1473,6 +1511,7 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
     rkv_pool_destroy(p);
     return s;
   }
+  p->done[0] = p->done[1] = 0;
   // zeroed pages: never-written slots hold finite codes and scales
   if (desc->page_memory == RKV_PAGES_DEVICE && (e = hipMemset(p->pages, 0, all_pages)) != hipSuccess) {
     rkv_pool_destroy(p);
@@ -1493,21 +1532,18 @@ rkv_status rkv_pool_create(rkv_ctx *ctx, const rkv_pool_desc *desc, rkv_pool **o
 rkv_status rkv_pool_destroy(rkv_pool *p) {
   if (!p) return RKV_OK;
   if (p->ctx) (void)hipSetDevice(p->ctx->device);
-  for (int i = 0; i < 2; ++i) {
-    if (p->stage_done[i]) (void)hipEventSynchronize(p->stage_done[i]);
-  }
+  // the last syncs' scatter kernels may still be reading the staging buffers
+  for (int i = 0; i < 2; ++i) (void)wait_stage(p, i);
   if (p->host_pages) (void)hipHostFree(p->host_pages);
   else (void)hipFree(p->pages);
   (void)hipFree(p->d_tables);
   (void)hipFree(p->d_lens);
-  (void)hipFree(p->d_stage[0]);
-  (void)hipFree(p->d_stage[1]);
+  (void)hipFree(p->scatter_count);
   (void)hipFree(p->d_crc);
   if (p->h_crc) (void)hipHostFree(p->h_crc);
-  for (int i = 0; i < 2; ++i) {
+  if (p->done) (void)hipHostFree(p->done);
+  for (int i = 0; i < 2; ++i)
     if (p->h_stage[i]) (void)hipHostFree(p->h_stage[i]);
-    if (p->stage_done[i]) (void)hipEventDestroy(p->stage_done[i]);
-  }
   if (p->handoff) (void)hipEventDestroy(p->handoff);
   rkv_alloc_destroy(p->alloc);
   delete p;
@@ -1544,13 +1580,26 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   // tables and copied pages, and earlier ones the old.  Nothing here waits
   // for the device unless the staging slot's kernels from two syncs ago are
   // still pending.
-  if (rkv_status s = order_after_last(p, as_stream(stream), op)) return s;
+  hipStream_t hs = as_stream(stream);
+  {
+    // the staging buffer is read in place when the kernel runs, so a graph
+    // replay would upload the tables of the capture, not the current ones
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(hs, &cap);
+    if (e != hipSuccess) return hip_fail(op, e);
+    if (cap != hipStreamCaptureStatusNone)
+      return fail(RKV_ERR_INVALID_ARG, op, "the stream is capturing a graph: table uploads carry "
+                  "host state and run eagerly, before the captured launches");
+  }
+  if (rkv_status s = order_after_last(p, hs, op)) return s;
   rkv_alloc *a = p->alloc;
   const int32_t W = a->d.max_pages_per_seq;
   const int32_t S = a->d.max_seqs;
   const uint32_t slot = p->n_syncs & 1u;
-  hipError_t e = hipEventSynchronize(p->stage_done[slot]);
-  if (e != hipSuccess) return hip_fail(op, e);
+  if (!wait_stage(p, (int)slot))
+    return fail(RKV_ERR_DEVICE, op, "the table upload of sync %llu never ran (device error)",
+                p->slot_sync[slot]);
+  hipError_t e = hipSuccess;
   int32_t *h = p->h_stage[slot];
   int32_t n_rows = 0;
   for (int32_t s = 0; s < S; ++s) {
@@ -1565,20 +1614,23 @@ rkv_status rkv_pool_sync_tables(rkv_pool *p, void *stream) {
   const size_t pairs_at = (size_t)n_rows * (W + 1) + S;
   int32_t n_pairs = 0;
   if (rkv_status s = rkv_alloc_take_copies(a, h + pairs_at, a->d.num_pages, &n_pairs)) return s;
-  const size_t bytes = sizeof(int32_t) * (pairs_at + 2 * (size_t)n_pairs);
-  hipStream_t hs = as_stream(stream);
-  int32_t *d = p->d_stage[slot];
-  if ((e = hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, hs)) != hipSuccess)
-    return hip_fail(op, e);
+  // the kernels read the staging buffer in place (pinned, coherent): no
+  // copy, and no event, in the stream; the copies run before the scatter,
+  // so the scatter's completion word covers both
+  const int32_t *d = p->d_stage[slot];
   ++p->n_syncs;
   if ((e = rkv::launch_copy_pages(p->pages, (int64_t)p->layer_bytes, p->d.layers, p->d.num_pages,
                                   d + pairs_at, n_pairs,
                                   (int64_t)rkv::page_bytes(to_geo(&p->g)), hs)) != hipSuccess)
     return hip_fail(op, e);
-  if ((e = rkv::launch_table_scatter(d, n_rows, W, S, p->d_tables, p->d_lens, hs)) != hipSuccess)
+  const unsigned long long blocks = (unsigned long long)n_rows + 1;
+  const unsigned long long seq = p->n_syncs;
+  if ((e = rkv::launch_table_scatter(d, n_rows, W, S, p->d_tables, p->d_lens, p->scatter_count,
+                                     p->scatter_blocks + blocks - 1, p->d_done + slot, seq, hs)) !=
+      hipSuccess)
     return hip_fail(op, e);
-  // the slot's host and device buffers are free again once this has run
-  if ((e = hipEventRecord(p->stage_done[slot], hs)) != hipSuccess) return hip_fail(op, e);
+  p->scatter_blocks += blocks;
+  p->slot_sync[slot] = seq;
   return RKV_OK;
 }
 
