@@ -78,6 +78,22 @@ __device__ __forceinline__ float dpp_ror8(float x) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
 }
 
+// The maximum of x over lanes li, li+16, li+32 and li+48 (the four 16-lane
+// rows), on every lane.  gfx950's row swaps hand each lane its partner's
+// value in a register: v_permlane16_swap pairs rows 0-1 and 2-3,
+// v_permlane32_swap the two halves.  Each swap leaves the lane's own and its
+// partner's value in the two outputs, in either order; the maximum does not
+// depend on which.  No LDS round trip (a shuffle by ds_bpermute waits on the
+// LDS queue, which the tile's scale reads also occupy).
+__device__ __forceinline__ float row_group_max(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__builtin_bit_cast(float, (uint32_t)a[0]), __builtin_bit_cast(float, (uint32_t)a[1]));
+  const uint32_t w = __builtin_bit_cast(uint32_t, x);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__builtin_bit_cast(float, (uint32_t)b[0]), __builtin_bit_cast(float, (uint32_t)b[1]));
+}
+
 // 4 stored V codes (one dword of x + 128 bytes) -> 4 exact f16 values x.
 __device__ __forceinline__ void v8x4_to_f16(uint32_t u, v2h &lo, v2h &hi) {
   const uint32_t l = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
@@ -426,18 +442,46 @@ struct Decoder {
       for (int m = 0; m < D / 16; ++m) oacc[np][m] *= f;
   }
 
+  // kKReg: V-code copies 0..K-1 of a tile (see issue); the immediate offset
+  // must be a constant expression, hence the recursion.
+  template <int K>
+  __device__ __forceinline__ static void copy_v_codes(const uint8_t *vsrc, lds_u8 *dst) {
+    if constexpr (K > 0) {
+      copy_v_codes<K - 1>(vsrc, dst);
+      constexpr int k = K - 1;
+      __builtin_amdgcn_global_load_lds(vsrc + 4096 * (k / 4), dst + 4096 * (k / 4), 16, 1024 * (k % 4), kCpol);
+    }
+  }
+
   // Copy tile `tile` (32 tokens) of this work unit HBM -> LDS stage `dst`.
   // Page ids come from `pidv` (lane i holds the partition's i-th page id).
   __device__ __forceinline__ void issue(int tile, lds_u8 *dst) {
     const Geo &g = p.g;
     const int32_t t0 = tok0 + tile * kTile;
-    const int32_t pi = t0 / g.page_tokens - pg_first;
+    // page_tokens is a power of two (checked on the host): shifts, not the
+    // generic signed division
+    const int32_t psh = __builtin_ctz((uint32_t)g.page_tokens);
+    const int32_t pi = (t0 >> psh) - pg_first;
     using PL = ChunkPlan<D, kSmall, kKReg, NW>;
     if constexpr (!kSmall) {
       const int32_t pid = kPageList ? __builtin_amdgcn_readfirstlane(pg_lds[pi])
                                     : __builtin_amdgcn_readlane(pidv, pi);
       const uint8_t *base = kv_base + (uint64_t)pid * PB;
-      const uint32_t s0 = (uint32_t)(t0 % g.page_tokens);
+      const uint32_t s0 = (uint32_t)(t0 & (g.page_tokens - 1));
+      if constexpr (kKReg) {
+        // The V codes of a tile are 32*D contiguous bytes (D rows of 32
+        // slots), copied to the stage's first 32*D bytes: 2D/64 copies from
+        // one lane address at offsets of 1 KiB.  The copy's immediate offset
+        // moves the global and the LDS address alike, so the copies of each
+        // 4 KiB group share one address register and one M0.  The last copy
+        // carries the K and V scale runs (plan entry 2D/64).
+        constexpr int kNV = 2 * D / 64;
+        static_assert(S::kInstr == kNV + 1, "V codes, then one copy of both scale runs");
+        copy_v_codes<kNV>(base + plan.off[0] + s0 * (uint32_t)D, dst);
+        __builtin_amdgcn_global_load_lds(base + plan.off[kNV] + s0 * (uint32_t)(D / 16),
+                                         dst + PL::dst16(kNV), 16, 0, kCpol);
+        return;
+      }
       // this wave's copies k = i*NW + wave, entry i of its plan
 #pragma unroll
       for (int i = 0; i < PL::kPer; ++i) {
@@ -579,9 +623,10 @@ struct Decoder {
   __device__ __forceinline__ void load_k(int tile) {
     const Geo &g = p.g;
     const int32_t t0 = tok0 + tile * kTile;
-    const int32_t pid = __builtin_amdgcn_readlane(pidv, t0 / g.page_tokens - pg_first);
+    const int32_t psh = __builtin_ctz((uint32_t)g.page_tokens);
+    const int32_t pid = __builtin_amdgcn_readlane(pidv, (t0 >> psh) - pg_first);
     const uint8_t *base = kv_base + (uint64_t)pid * PB +
-                          (uint64_t)((t0 % g.page_tokens) + li) * D + (kWide ? 8 : 16) * lg;
+                          (uint64_t)((t0 & (g.page_tokens - 1)) + li) * D + (kWide ? 8 : 16) * lg;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -791,8 +836,7 @@ struct Decoder {
             tmax = fmaxf(tmax, sv);
           }
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      tmax = row_group_max(tmax);
       const bool need = tmax > mref[np] + kTau;  // also true for the first visible tile
       if (__any(need)) {
         const float mnew = need ? tmax : mref[np];
@@ -939,8 +983,7 @@ struct Decoder {
           tmax = fmaxf(tmax, sv);
         }
     }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    tmax = row_group_max(tmax);
     const bool need = tmax > mref[0] + kTau;  // also true for the first visible tile
     float alpha = 1.0f;
     if (__any(need)) {
