@@ -331,6 +331,7 @@ struct Decoder {
   int32_t seq, len, tok0, tok_end, n_tiles;
   int32_t app_mode;        // 0: no rows to append here; 1: before the first copy; 2: after the prologue copies
   int32_t app_first;       // first tile of this partition that holds an appended row
+  bool issued0 = false;    // kKReg: tile 0's copies and K codes went out in the prologue
   int32_t pg_first;        // first page index (within the sequence) of the partition
   int32_t pidv;            // lane i: page id of the partition's i-th page
   uint64_t pid_bad;        // lanes whose page id was out of range (replaced by page 0)
@@ -1428,10 +1429,11 @@ struct Decoder {
   __device__ __forceinline__ void run(lds_u8 *__restrict__ s0, lds_u8 *__restrict__ s1,
                                       lds_u8 *__restrict__ s2) {
     if constexpr (kKReg) {
-      // The appended rows' source values are loaded first, with the
-      // prologue's loads still landing.  Position in tile 0 (app_mode 1):
-      // they are quantized and stored, and the stores complete, before tile
-      // 0's copies are issued.  Later tiles (app_mode 2): tile 0 is peeled
+      // Tile 0's copies and K codes normally went out in the prologue
+      // (issued0).  The appended rows' source values are loaded next, with
+      // the prologue's loads still landing.  Position in tile 0 (app_mode
+      // 1): they are quantized and stored, and the stores complete, before
+      // tile 0's copies are issued here.  Later tiles (app_mode 2): tile 0 is peeled
       // off the loop and they are stored after its wait, before its compute;
       // the vmcnt(0) of step 1 drains them before tile 2's copies, and a
       // drain in compute(0) precedes tile 1's when a row lies there.
@@ -1442,9 +1444,14 @@ struct Decoder {
         app_store(av, alive);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
-      if (n_tiles == 0) return;
-      issue(0, s0);
-      load_k(0);
+      if (n_tiles == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the prologue's copies
+        return;
+      }
+      if (!issued0) {
+        issue(0, s0);
+        load_k(0);
+      }
       __builtin_amdgcn_s_waitcnt(kWaitBase);
       if (app_mode == 2) app_store(av, alive);
       compute(0, s0, s1, app_mode == 2 && app_first == 1);
@@ -1511,16 +1518,18 @@ __device__ __forceinline__ void q_split(float u, uint32_t &hi8, uint32_t &md8, u
   lo8 = (uint32_t)(uint8_t)(int8_t)lo;
 }
 
+// The raw query words of one lane for load_q_planes' split: bf16 pairs in
+// words 0..7 of each 64-dim step, or f32 bits in 0..15 (zeros for a dead
+// row).  Loaded apart from the split so that a caller can issue other loads
+// in between: nothing reads the words before split_q_planes.
 template <int D>
-__device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t qbase, int li,
-                                              int lg, float scale_log2, v4i *qhi, v4i *qmd,
-                                              v4i *qlo, float &qmul) {
+__device__ __forceinline__ void load_q_raw(const void *qp, bool bf16, int64_t qbase, int lg,
+                                           uint32_t (&qw)[D / 64][16]) {
   constexpr int NC = D / 64;
-  float qv[NC][16];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) qv[c][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) qw[c][e] = 0u;
   if (qbase >= 0) {
     const int64_t base = qbase + 16 * lg;
     if (bf16) {
@@ -1529,34 +1538,45 @@ __device__ __forceinline__ void load_q_planes(const void *qp, bool bf16, int64_t
       for (int c = 0; c < NC; ++c) {
         const uint4 w0 = *reinterpret_cast<const uint4 *>(q + 64 * c);
         const uint4 w1 = *reinterpret_cast<const uint4 *>(q + 64 * c + 8);
-        const uint32_t ws[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          qv[c][2 * e] = bf16_bits_to_f32((uint16_t)(ws[e] & 0xffffu));
-          qv[c][2 * e + 1] = bf16_bits_to_f32((uint16_t)(ws[e] >> 16));
-        }
+        qw[c][0] = w0.x, qw[c][1] = w0.y, qw[c][2] = w0.z, qw[c][3] = w0.w;
+        qw[c][4] = w1.x, qw[c][5] = w1.y, qw[c][6] = w1.z, qw[c][7] = w1.w;
       }
     } else {
-      const float *q = static_cast<const float *>(qp) + base;
+      const uint32_t *q = static_cast<const uint32_t *>(qp) + base;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
-          const float4 w = *reinterpret_cast<const float4 *>(q + 64 * c + 4 * e4);
-          qv[c][4 * e4] = w.x;
-          qv[c][4 * e4 + 1] = w.y;
-          qv[c][4 * e4 + 2] = w.z;
-          qv[c][4 * e4 + 3] = w.w;
+          const uint4 w = *reinterpret_cast<const uint4 *>(q + 64 * c + 4 * e4);
+          qw[c][4 * e4] = w.x, qw[c][4 * e4 + 1] = w.y, qw[c][4 * e4 + 2] = w.z, qw[c][4 * e4 + 3] = w.w;
         }
     }
   }
+}
+template <int D>
+__device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][16], bool bf16, int li,
+                                               int lg, float scale_log2, v4i *qhi, v4i *qmd,
+                                               v4i *qlo, float &qmul) {
+  constexpr int NC = D / 64;
+  float qv[NC][16];
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      if (bf16) {
+        qv[c][2 * e] = bf16_bits_to_f32((uint16_t)(qw[c][e] & 0xffffu));
+        qv[c][2 * e + 1] = bf16_bits_to_f32((uint16_t)(qw[c][e] >> 16));
+      } else {
+        qv[c][2 * e] = __uint_as_float(qw[c][2 * e]);
+        qv[c][2 * e + 1] = __uint_as_float(qw[c][2 * e + 1]);
+      }
+    }
   float amax = 0.0f;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
     for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
-  amax = fmaxf(amax, __shfl_xor(amax, 16));
-  amax = fmaxf(amax, __shfl_xor(amax, 32));
+  amax = row_group_max(amax);
   const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
   qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
   const bool live = (li < 8) == (lg < 2);
@@ -1970,11 +1990,15 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   } else if constexpr (Dec::kWide) {
     load_q_wide<D>(p.q, p.q_bf16 != 0, qrow(r0 + li), lg, p.scale_log2, dc.qhi[0], dc.qmd[0],
                    dc.qlo[0], qmul[0]);
-  } else {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt)
-      load_q_planes<D>(p.q, p.q_bf16 != 0, qrow(r0 + 8 * nt + (li & 7)), li, lg, p.scale_log2,
-                       dc.qhi[nt], dc.qmd[nt], dc.qlo[nt], qmul[nt]);
+  }
+  // The 8-row three-plane query: its words are loaded here and split below,
+  // after tile 0's copies went out (kKReg), so the split overlaps their
+  // latency.
+  constexpr bool kPlanes = !(Dec::kDSplit || kQF16 || Dec::kWide);
+  uint32_t qw[D / 64][16];
+  if constexpr (kPlanes) {
+    static_assert(NT == 1, "the three-plane split with one n-tile");
+    load_q_raw<D>(p.q, p.q_bf16 != 0, qrow(r0 + (li & 7)), lg, qw);
   }
 
   const bool pid_bad = pid < 0 || pid >= g.num_pages;
@@ -2005,6 +2029,23 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) dc.apos[j] = app_seq[j] == seq ? app_pos[j] : -1;
   }
+
+  // kKReg: tile 0's copies and K codes go out now, ahead of the query split,
+  // unless an appended row must be stored into tile 0 first (app_mode 1,
+  // done in run()).  Branch-free, so that the wait for the query words
+  // after it does not also drain every copy on one side of a branch: with
+  // app_mode 1 the copies are a throwaway prefetch into stage 1 (run()
+  // drains them, copies tile 0 after the stores, and tile 1 overwrites
+  // stage 1); an empty partition reads page 0, and run() drains that too.
+  if constexpr (kKReg) {
+    const bool mode1 = __builtin_amdgcn_readfirstlane(dc.app_mode) == 1;
+    dc.issue(0, (lds_u8 *)lds[mode1 ? 1 : 0]);
+    dc.load_k(0);
+    dc.issued0 = !mode1;
+  }
+  if constexpr (kPlanes)
+    split_q_planes<D>(qw, p.q_bf16 != 0, li, lg, p.scale_log2, dc.qhi[0], dc.qmd[0], dc.qlo[0],
+                      qmul[0]);
 
   // ---- per-lane softmax rows: PV n-tile np, column li -> row 16*np + li ---
 #pragma unroll
