@@ -1518,35 +1518,37 @@ __device__ __forceinline__ void q_split(float u, uint32_t &hi8, uint32_t &md8, u
   lo8 = (uint32_t)(uint8_t)(int8_t)lo;
 }
 
-// The raw query words of one lane for load_q_planes' split: bf16 pairs in
-// words 0..7 of each 64-dim step, or f32 bits in 0..15 (zeros for a dead
-// row).  Loaded apart from the split so that a caller can issue other loads
-// in between: nothing reads the words before split_q_planes.
+// The three-plane split of the 8-row query in two steps: load_q_raw loads
+// the words, split_q_planes splits them, so that a caller can issue other
+// loads in between (nothing reads the words before the split).  Lanes li
+// and li ^ 8 serve the same row and dims and exactly one of them is live, so
+// each loads and splits half of the 16 elements -- elements 8h .. 8h+7, h =
+// li >> 3 -- and the live lane takes the other half's plane words from its
+// partner over a DPP row rotation; the dead lane's words are zeros.
+// Raw words: bf16 pairs in 0..3, or f32 bits in 0..7, per 64-dim step.
 template <int D>
-__device__ __forceinline__ void load_q_raw(const void *qp, bool bf16, int64_t qbase, int lg,
-                                           uint32_t (&qw)[D / 64][16]) {
+__device__ __forceinline__ void load_q_raw(const void *qp, bool bf16, int64_t qbase, int li, int lg,
+                                           uint32_t (&qw)[D / 64][8]) {
   constexpr int NC = D / 64;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) qw[c][e] = 0u;
+    for (int e = 0; e < 8; ++e) qw[c][e] = 0u;
   if (qbase >= 0) {
-    const int64_t base = qbase + 16 * lg;
+    const int64_t base = qbase + 16 * lg + 8 * (li >> 3);
     if (bf16) {
       const uint16_t *q = static_cast<const uint16_t *>(qp) + base;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        const uint4 w0 = *reinterpret_cast<const uint4 *>(q + 64 * c);
-        const uint4 w1 = *reinterpret_cast<const uint4 *>(q + 64 * c + 8);
-        qw[c][0] = w0.x, qw[c][1] = w0.y, qw[c][2] = w0.z, qw[c][3] = w0.w;
-        qw[c][4] = w1.x, qw[c][5] = w1.y, qw[c][6] = w1.z, qw[c][7] = w1.w;
+        const uint4 w = *reinterpret_cast<const uint4 *>(q + 64 * c);
+        qw[c][0] = w.x, qw[c][1] = w.y, qw[c][2] = w.z, qw[c][3] = w.w;
       }
     } else {
       const uint32_t *q = static_cast<const uint32_t *>(qp) + base;
 #pragma unroll
       for (int c = 0; c < NC; ++c)
 #pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
+        for (int e4 = 0; e4 < 2; ++e4) {
           const uint4 w = *reinterpret_cast<const uint4 *>(q + 64 * c + 4 * e4);
           qw[c][4 * e4] = w.x, qw[c][4 * e4 + 1] = w.y, qw[c][4 * e4 + 2] = w.z, qw[c][4 * e4 + 3] = w.w;
         }
@@ -1554,15 +1556,15 @@ __device__ __forceinline__ void load_q_raw(const void *qp, bool bf16, int64_t qb
   }
 }
 template <int D>
-__device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][16], bool bf16, int li,
+__device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][8], bool bf16, int li,
                                                int lg, float scale_log2, v4i *qhi, v4i *qmd,
                                                v4i *qlo, float &qmul) {
   constexpr int NC = D / 64;
-  float qv[NC][16];
+  float qv[NC][8];
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < 4; ++e) {
       if (bf16) {
         qv[c][2 * e] = bf16_bits_to_f32((uint16_t)(qw[c][e] & 0xffffu));
         qv[c][2 * e + 1] = bf16_bits_to_f32((uint16_t)(qw[c][e] >> 16));
@@ -1575,25 +1577,39 @@ __device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][16],
 #pragma unroll
   for (int c = 0; c < NC; ++c)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
+  amax = fmaxf(amax, dpp_ror8(amax));  // the partner's half of the chunks
   amax = row_group_max(amax);
   const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
   qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
   const bool live = (li < 8) == (lg < 2);
+  const bool upper = li >= 8;  // this lane split elements 8..15
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    uint32_t hw[4] = {0, 0, 0, 0}, mw[4] = {0, 0, 0, 0}, lw[4] = {0, 0, 0, 0};
+    uint32_t w[3][2] = {{0, 0}, {0, 0}, {0, 0}};  // plane, word: own elements
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      uint32_t h8, m8, l8;
-      q_split(live ? qv[c][e] * inv : 0.0f, h8, m8, l8);
-      hw[e >> 2] |= h8 << (8 * (e & 3));
-      mw[e >> 2] |= m8 << (8 * (e & 3));
-      lw[e >> 2] |= l8 << (8 * (e & 3));
+    for (int e = 0; e < 8; ++e) {
+      uint32_t b[3];
+      q_split(qv[c][e] * inv, b[0], b[1], b[2]);
+#pragma unroll
+      for (int pl = 0; pl < 3; ++pl) w[pl][e >> 2] |= b[pl] << (8 * (e & 3));
     }
-    qhi[c] = v4i{(int)hw[0], (int)hw[1], (int)hw[2], (int)hw[3]};
-    qmd[c] = v4i{(int)mw[0], (int)mw[1], (int)mw[2], (int)mw[3]};
-    qlo[c] = v4i{(int)lw[0], (int)lw[1], (int)lw[2], (int)lw[3]};
+    v4i out[3];
+#pragma unroll
+    for (int pl = 0; pl < 3; ++pl) {
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint32_t part = __builtin_bit_cast(
+            uint32_t, __builtin_amdgcn_update_dpp(0, (int)w[pl][k], 0x128, 0xf, 0xf, false));  // row_ror:8
+        o[k] = live ? (upper ? part : w[pl][k]) : 0u;
+        o[2 + k] = live ? (upper ? w[pl][k] : part) : 0u;
+      }
+      out[pl] = v4i{(int)o[0], (int)o[1], (int)o[2], (int)o[3]};
+    }
+    qhi[c] = out[0];
+    qmd[c] = out[1];
+    qlo[c] = out[2];
   }
 }
 
@@ -1995,10 +2011,10 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
   // after tile 0's copies went out (kKReg), so the split overlaps their
   // latency.
   constexpr bool kPlanes = !(Dec::kDSplit || kQF16 || Dec::kWide);
-  uint32_t qw[D / 64][16];
+  uint32_t qw[D / 64][8];
   if constexpr (kPlanes) {
     static_assert(NT == 1, "the three-plane split with one n-tile");
-    load_q_raw<D>(p.q, p.q_bf16 != 0, qrow(r0 + (li & 7)), lg, qw);
+    load_q_raw<D>(p.q, p.q_bf16 != 0, qrow(r0 + (li & 7)), li, lg, qw);
   }
 
   const bool pid_bad = pid < 0 || pid >= g.num_pages;
