@@ -52,13 +52,14 @@ def load_rkv():
 
 
 class GpuState:
-    """The GPU's graphics and memory clocks and its socket power, sampled
-    through amdsmi on a side thread every `period` seconds while a timed
-    region runs, plus its power cap and clock limits: so that a line from a
-    slower-clocked or power-capped box can be told apart from a slower
-    build.  Any amdsmi failure is reported in the result, never raised."""
+    """The GPU's power cap and clock limits through amdsmi, so that a line
+    from a power-capped or lower-clocked box can be told apart from a slower
+    build; start() and stop() also sample the graphics and memory clocks and
+    the socket power every `period` seconds on a side thread (amdsmi updates
+    them on a scale of many ms, so they describe long regions only).  Any
+    amdsmi failure is reported in the result, never raised."""
 
-    def __init__(self, period=0.02):
+    def __init__(self, period=0.005):
         import threading
         self.period, self.samples, self.static, self.error = period, [], {}, None
         self._stop = threading.Event()
@@ -110,21 +111,20 @@ class GpuState:
             pass
 
     def start(self):
-        """One sample now (the warm-up has just run), then one every period."""
+        """Sample every period on a side thread until stop().  No sample at
+        the start or the stop: with the stream drained around a region the
+        clocks read there are idle clocks."""
         import threading
-        if self.h is not None and self.error is None and self._one():
+        if self.h is not None and self.error is None:
             self._thread = threading.Thread(target=self._sample, daemon=True)
             self._thread.start()
         return self
 
     def stop(self) -> dict:
-        """Stop sampling, with one last sample (a short region may end before
-        the first period)."""
         import numpy as np
         if self._thread is not None:
             self._stop.set()
             self._thread.join()
-            self._one()
         res = dict(self.static)
         if self.samples:
             for i, k in enumerate(("gfx_clk_mhz", "mem_clk_mhz", "socket_power_w")):
@@ -149,6 +149,9 @@ def parse():
     ap.add_argument("--no-secondary", dest="secondary", action="store_false",
                     help="headline only: skip configs 2, 3 and 5 in the default line")
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--sustained-ms", type=float, default=150.0,
+                    help="headline: length of the sustained pass (the step back to back) after "
+                         "the timed region")
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=32768)
     ap.add_argument("--q-heads", type=int, default=16)
@@ -285,13 +288,13 @@ def main() -> int:
         for x in e:
             x.record(stream)
     torch.cuda.synchronize()
-    gpu = GpuState().start()
+    gpu = GpuState()
+    gpu_state = gpu.stop()  # clock limits and power cap (no sampler in the timed region)
     t0 = time.perf_counter()
     for i in range(args.steps):
         step(evs.get(i))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_state = gpu.stop()
     ctx.sync()
     # the event pass: every step with its events (markers cost the stream a
     # few us per step, so it runs after the timed region), for percentiles
@@ -305,6 +308,20 @@ def main() -> int:
     for e in pass_evs:
         step(e)
     torch.cuda.synchronize()
+    ctx.sync()
+    # the sustained pass: the same step back to back for about
+    # --sustained-ms.  The graphics clock falls within a few ms of sustained
+    # load and partly recovers later (power management; amdsmi's clock
+    # readings are too coarse in time to follow it), and while it is below
+    # about 1.5 GHz the decode's per-tile instruction stream, not HBM, sets
+    # its pace.  A short timed region can fall in that dip; this records the
+    # steady rate beside it.
+    n_sus = max(20, int(args.sustained_ms * 1e-3 / max(wall / args.steps, 1e-6)))
+    t0 = time.perf_counter()
+    for _ in range(n_sus):
+        step()
+    torch.cuda.synchronize()
+    sus_s = (time.perf_counter() - t0) / n_sus
     ctx.sync()
     part = int(ws[:4].view(torch.int32).item())  # the partition length the device chose
     n_parts = (L + part - 1) // part
@@ -369,6 +386,8 @@ def main() -> int:
                       "event_step_p10_p50_p90": _pcts(p_step),
                       "percentile_samples": n_pass},
         "gpu_state": gpu_state,
+        "sustained": {"steps": n_sus, "us_per_step": round(sus_s * 1e6, 2),
+                      "gbs": round(step_bytes / sus_s / 1e9, 2)},
         "split_k_partial_bytes": partial_bytes,
         "achieved_tflops": round(flops / step_s / 1e12, 2),
         "roofline": {"bound": "hbm", "kernel": "rkv::decode_kernel<256, 1, false, 2, 1, false>",

@@ -78,6 +78,18 @@ __device__ __forceinline__ float dpp_ror8(float x) {
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
 }
 
+// The second f16 term of a pair of PV weights p0, p1 whose first terms are
+// h = f16(p): f16(p - h), where p - h is exact in f32.  Computed as
+// fma(h, m1, p) with the f16 halves of h as v_fma_mix operands (one
+// instruction per value, where a conversion back to f32 and a subtraction
+// take two); m1 = -1 comes from a register so that the compiler keeps the
+// fma instead of rewriting it into that subtraction.
+__device__ __forceinline__ v2h p_residual(v2h h, float p0, float p1) {
+  float m1;
+  asm("v_mov_b32 %0, -1.0" : "=v"(m1));
+  return v2h{(_Float16)__builtin_fmaf((float)h[0], m1, p0), (_Float16)__builtin_fmaf((float)h[1], m1, p1)};
+}
+
 // The maximum of x over lanes li, li+16, li+32 and li+48 (the four 16-lane
 // rows), on every lane.  gfx950's row swaps hand each lane its partner's
 // value in a register: v_permlane16_swap pairs rows 0-1 and 2-3,
@@ -862,7 +874,7 @@ struct Decoder {
         const v2h h2 = {(_Float16)pr[2 * i], (_Float16)pr[2 * i + 1]};
         pp[np][i] = __builtin_bit_cast(uint32_t, h2);
         if constexpr (kSplitP) {
-          const v2h l2 = {(_Float16)(pr[2 * i] - (float)h2[0]), (_Float16)(pr[2 * i + 1] - (float)h2[1])};
+          const v2h l2 = p_residual(h2, pr[2 * i], pr[2 * i + 1]);
           pl[np][i] = __builtin_bit_cast(uint32_t, l2);
           if constexpr (kColSplit) {
             // columns 0-7 take p and no second term: zero their p_lo and
@@ -1008,7 +1020,7 @@ struct Decoder {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const v2h h2 = {(_Float16)pr[2 * i], (_Float16)pr[2 * i + 1]};
-      const v2h l2 = {(_Float16)(pr[2 * i] - (float)h2[0]), (_Float16)(pr[2 * i + 1] - (float)h2[1])};
+      const v2h l2 = p_residual(h2, pr[2 * i], pr[2 * i + 1]);
       pq[w][i] = __builtin_bit_cast(uint32_t, h2);
       pq[w][4 + i] = __builtin_bit_cast(uint32_t, l2);
     }
