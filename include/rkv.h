@@ -114,6 +114,18 @@ rkv_status rkv_seq_reserve(rkv_alloc *a, int32_t seq, int32_t new_len);
  * page_tokens) (speculative rollback, har-execution/src/speculation.rs:55,172). */
 rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len);
 rkv_status rkv_seq_free(rkv_alloc *a, int32_t seq);
+/* rkv_seq_reserve / rkv_seq_truncate over n (seq, new_len) pairs (host
+ * arrays), in order: one call where a serving step grows or rolls back every
+ * running sequence.  Stops at the first failing pair and returns its status
+ * (with that pair named in rkv_last_error); the pairs before it have taken
+ * effect.  *done (may be NULL) = the number of pairs applied.  No
+ * counterpart in the reference, whose scheduler records pages one sequence
+ * at a time (har-serve/src/scheduler.rs:1045-1077); for callers where each
+ * foreign call costs more than the allocator's work. */
+rkv_status rkv_seq_reserve_n(rkv_alloc *a, int32_t n, const int32_t *seqs, const int32_t *new_lens,
+                             int32_t *done);
+rkv_status rkv_seq_truncate_n(rkv_alloc *a, int32_t n, const int32_t *seqs, const int32_t *new_lens,
+                              int32_t *done);
 rkv_status rkv_seq_len(const rkv_alloc *a, int32_t seq, int32_t *len);
 rkv_status rkv_block_table_get(const rkv_alloc *a, int32_t seq, int32_t *out,
                                int32_t cap, int32_t *n);

@@ -145,6 +145,8 @@ _SIGS = {
     "rkv_alloc_destroy": (C.c_int32, [P]),
     "rkv_seq_reserve": (C.c_int32, [P, C.c_int32, C.c_int32]),
     "rkv_seq_truncate": (C.c_int32, [P, C.c_int32, C.c_int32]),
+    "rkv_seq_reserve_n": (C.c_int32, [P, C.c_int32, I32P, I32P, I32P]),
+    "rkv_seq_truncate_n": (C.c_int32, [P, C.c_int32, I32P, I32P, I32P]),
     "rkv_seq_free": (C.c_int32, [P, C.c_int32]),
     "rkv_seq_len": (C.c_int32, [P, C.c_int32, I32P]),
     "rkv_block_table_get": (C.c_int32, [P, C.c_int32, I32P, C.c_int32, I32P]),
@@ -327,6 +329,26 @@ class Allocator:
 
     def truncate(self, seq: int, new_len: int) -> None:
         check(lib().rkv_seq_truncate(self.h, seq, new_len))
+
+    def _apply_n(self, fn, seqs, new_lens) -> int:
+        import numpy as np
+        s = np.ascontiguousarray(seqs, dtype=np.int32)
+        n = np.ascontiguousarray(new_lens, dtype=np.int32)
+        if s.shape != n.shape or s.ndim != 1:
+            raise ValueError("seqs and new_lens must be 1-D and of one length")
+        done = C.c_int32(0)
+        st = fn(self.h, int(s.size), s.ctypes.data_as(I32P), n.ctypes.data_as(I32P), C.byref(done))
+        check(st)
+        return done.value
+
+    def reserve_n(self, seqs, new_lens) -> int:
+        """rkv_seq_reserve_n: every (seq, new_len) pair in order, stopping at
+        the first failure (raised; the pairs before it have taken effect)."""
+        return self._apply_n(lib().rkv_seq_reserve_n, seqs, new_lens)
+
+    def truncate_n(self, seqs, new_lens) -> int:
+        """rkv_seq_truncate_n: as reserve_n, rolling back."""
+        return self._apply_n(lib().rkv_seq_truncate_n, seqs, new_lens)
 
     def free(self, seq: int) -> None:
         check(lib().rkv_seq_free(self.h, seq))

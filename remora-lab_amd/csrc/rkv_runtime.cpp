@@ -364,6 +364,35 @@ rkv_status rkv_seq_truncate(rkv_alloc *a, int32_t seq, int32_t new_len) {
 
 rkv_status rkv_seq_free(rkv_alloc *a, int32_t seq) { return rkv_seq_truncate(a, seq, 0); }
 
+// The _n forms: each pair through the single form, in order, stopping at
+// the first failure (whose message names the pair).
+static rkv_status seq_apply_n(rkv_alloc *a, int32_t n, const int32_t *seqs, const int32_t *new_lens,
+                              int32_t *done, const char *op,
+                              rkv_status (*one)(rkv_alloc *, int32_t, int32_t)) {
+  if (done) *done = 0;
+  if (!a) return fail(RKV_ERR_INVALID_ARG, op, "allocator is NULL");
+  if (n < 0) return fail(RKV_ERR_INVALID_ARG, op, "n=%d", n);
+  if (n > 0 && (!seqs || !new_lens)) return fail(RKV_ERR_INVALID_ARG, op, "seqs or new_lens is NULL");
+  for (int32_t i = 0; i < n; ++i) {
+    if (rkv_status st = one(a, seqs[i], new_lens[i])) {
+      const std::string inner = g_last_error;
+      return fail(st, op, "pair %d (seq %d, new_len %d): %s", i, seqs[i], new_lens[i], inner.c_str());
+    }
+    if (done) *done = i + 1;
+  }
+  return RKV_OK;
+}
+
+rkv_status rkv_seq_reserve_n(rkv_alloc *a, int32_t n, const int32_t *seqs, const int32_t *new_lens,
+                             int32_t *done) {
+  return seq_apply_n(a, n, seqs, new_lens, done, "rkv_seq_reserve_n", rkv_seq_reserve);
+}
+
+rkv_status rkv_seq_truncate_n(rkv_alloc *a, int32_t n, const int32_t *seqs, const int32_t *new_lens,
+                              int32_t *done) {
+  return seq_apply_n(a, n, seqs, new_lens, done, "rkv_seq_truncate_n", rkv_seq_truncate);
+}
+
 rkv_status rkv_seq_fork(rkv_alloc *a, int32_t src, int32_t dst, int32_t len) {
   const char *op = "rkv_seq_fork";
   if (rkv_status s = check_seq(a, src, op)) return s;

@@ -133,6 +133,47 @@ def test_allocator_errors(rkv):
     assert "rkv_seq_reserve" in rkv.lib().rkv_last_error().decode()
 
 
+def test_allocator_pair_batches(rkv):
+    """rkv_seq_reserve_n / rkv_seq_truncate_n apply their pairs in order,
+    exactly as the single calls would, and stop at the first failing pair
+    (which the error names), leaving the pairs before it applied."""
+    rng = np.random.default_rng(7)
+    one = rkv.Allocator(96, 16, 6, 16, seed=5)
+    many = rkv.Allocator(96, 16, 6, 16, seed=5)
+    lens = np.zeros(6, np.int64)
+    for _ in range(40):
+        seqs = rng.permutation(6)[: rng.integers(0, 7)].astype(np.int32)
+        grow = rng.random() < 0.6
+        new = np.array([lens[q] + rng.integers(0, 40) if grow else rng.integers(0, lens[q] + 1)
+                        for q in seqs], np.int32)
+        if grow and (sum(-(-int(x) // 16) for x in np.maximum(new, lens[seqs]))
+                     + sum(-(-int(lens[q]) // 16) for q in range(6) if q not in seqs)) > 96:
+            continue
+        for q, x in zip(seqs, new):
+            (one.reserve if grow else one.truncate)(int(q), int(x))
+        assert (many.reserve_n if grow else many.truncate_n)(seqs, new) == len(seqs)
+        lens[seqs] = new
+        for q in range(6):
+            assert one.block_table(q) == many.block_table(q)
+            assert one.seq_len(q) == many.seq_len(q) == lens[q]
+    # a failing pair stops the batch: earlier pairs applied, later ones not
+    a = rkv.Allocator(8, 16, 3, 4, seed=0)
+    seqs = np.array([0, 1, 2], np.int32)
+    new = np.array([20, 99, 5], np.int32)  # 99 tokens need 7 pages > max_pages_per_seq 4
+    done = C.c_int32(-1)
+    L = rkv.lib()
+    st = L.rkv_seq_reserve_n(a.h, 3, seqs.ctypes.data_as(rkv.I32P), new.ctypes.data_as(rkv.I32P),
+                             C.byref(done))
+    assert st == rkv.ERR_CAPACITY and done.value == 1
+    msg = L.rkv_last_error().decode()
+    assert "rkv_seq_reserve_n" in msg and "pair 1" in msg and "rkv_seq_reserve" in msg
+    assert (a.seq_len(0), a.seq_len(1), a.seq_len(2)) == (20, 0, 0)
+    assert L.rkv_seq_truncate_n(a.h, 0, None, None, None) == rkv.OK
+    assert L.rkv_seq_truncate_n(a.h, 2, None, None, None) == rkv.ERR_INVALID_ARG
+    assert L.rkv_seq_truncate_n(None, 1, seqs.ctypes.data_as(rkv.I32P), new.ctypes.data_as(rkv.I32P),
+                                None) == rkv.ERR_INVALID_ARG
+
+
 def _ws(rkv, g, B, L, q_heads, q_len=1, pt=0):
     a = rkv.DecodeArgs(B, None, None, rkv.BF16, q_len, q_heads, 1.0, None, rkv.F32, pt, L, None, 0,
                        None, None)
