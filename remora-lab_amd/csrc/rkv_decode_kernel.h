@@ -1118,32 +1118,48 @@ struct Decoder {
   __device__ __forceinline__ void pv_weights(const v4i sv, const uint32_t (&pp)[NP][4],
                                              const uint32_t (&pl)[NP][4], const uint32_t (&pz)[NP][4],
                                              v8h (&pb)[NP], v8h (&pbl)[NP]) const {
+    // Step by step across the four pairs: each step depends on the one
+    // before, and back-to-back dependent packed-f16 operations take wait
+    // states (s_nop) that four independent pairs in between hide.
 #pragma unroll
     for (int np = 0; np < NP; ++np) {
+      v2h ph[4], dv[4], q[4], e[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const v2h ph = __builtin_bit_cast(v2h, pp[np][i]);
-        const v2h dv = __builtin_bit_cast(v2h, (uint32_t)sv[i]);
-        v2h hi;
-        if constexpr (kColSplit) {
-          // lanes li < 8: q = 0, so e = f16(p)*d_v rounded once and the
-          // second fma adds 0 * d_v; lanes li >= 8: e is the product's
-          // exact rounding error and the result the second weight term
-          const v2h q = __builtin_bit_cast(v2h, pz[np][i]) * dv;
-          const v2h e = __builtin_elementwise_fma(ph, dv, -q);
-          hi = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, e);
-        } else {
-          const v2h prod = ph * dv;
-          hi = prod;
-          if constexpr (kSplitP) {
-            const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
-            const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv, err);
+        ph[i] = __builtin_bit_cast(v2h, pp[np][i]);
+        dv[i] = __builtin_bit_cast(v2h, (uint32_t)sv[i]);
+      }
+      if constexpr (kColSplit) {
+        // lanes li < 8: q = 0, so e = f16(p)*d_v rounded once and the
+        // second fma adds 0 * d_v; lanes li >= 8: e is the product's
+        // exact rounding error and the result the second weight term
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = __builtin_bit_cast(v2h, pz[np][i]) * dv[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) e[i] = __builtin_elementwise_fma(ph[i], dv[i], -q[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v2h hi = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv[i], e[i]);
+          pb[np][2 * i] = hi[0];
+          pb[np][2 * i + 1] = hi[1];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          q[i] = ph[i] * dv[i];
+          pb[np][2 * i] = q[i][0];
+          pb[np][2 * i + 1] = q[i][1];
+        }
+        if constexpr (kSplitP) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) e[i] = __builtin_elementwise_fma(ph[i], dv[i], -q[i]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pl[np][i]), dv[i], e[i]);
             pbl[np][2 * i] = lo[0];
             pbl[np][2 * i + 1] = lo[1];
           }
         }
-        pb[np][2 * i] = hi[0];
-        pb[np][2 * i + 1] = hi[1];
       }
     }
   }
