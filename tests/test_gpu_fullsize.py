@@ -136,9 +136,10 @@ def run_decode(rkv, pool, layer, q, out, seq_ids, max_len, q_len=1, app=None,
 
 
 def _decode_step_check(rkv, rko, ctx, big, layer, lens, sample, q_np, q_d, out, app_rows,
-                       partition_tokens=0, label=""):
+                       partition_tokens=0, label="", expect_pt=None):
     """One decode launch (this step's row appended inside it) on `layer`;
-    checks the appended rows and the sampled sequences' outputs."""
+    checks the appended rows and the sampled sequences' outputs (and, with
+    expect_pt, the partition length the device chose)."""
     torch = _torch()
     B = len(lens)
     sid = torch.arange(B, dtype=torch.int32, device="cuda")
@@ -149,6 +150,8 @@ def _decode_step_check(rkv, rko, ctx, big, layer, lens, sample, q_np, q_d, out, 
                     partition_tokens=partition_tokens)
     ctx.sync()
     parts = int(ws[:4].view(torch.int32).item()) if partition_tokens == 0 else partition_tokens
+    if expect_pt is not None:
+        assert parts == expect_pt, f"{label}: the device chose {parts}-token partitions"
     got = out.float().cpu().numpy()
     kn_h, vn_h = kn.float().cpu().numpy(), vn.float().cpu().numpy()
     errs = []
@@ -221,13 +224,14 @@ def test_fullsize_config2(rkv, rko, ctx):
 
 @pytest.mark.parametrize("partition_tokens", [0, 2048])
 def test_fullsize_config3(rkv, rko, ctx, partition_tokens):
-    """Config 3: one sequence of 262,144 tokens (the last appended by the
-    decode launch), Hq 16 / Hkv 2, D 256: device-chosen partitions (482 of 544
-    tokens at this length, merged by the one-launch combine) and the
-    reference's 128 partitions of 2048 tokens; all 16 heads checked, for an
-    N(0,1) query and one with outlier channels."""
+    """Config 3: one sequence of 262,145 tokens (the last appended by the
+    decode launch, as in bench.py's config 3), Hq 16 / Hkv 2, D 256:
+    device-chosen partitions (482 of 544 tokens, the last one 481, merged by
+    the one-launch combine) and the reference's partitions of 2048 tokens
+    (129, the last one 1 token); all 16 heads checked, for an N(0,1) query
+    and one with outlier channels."""
     torch = _torch()
-    L = 262144
+    L = 262145
     print(f"config3 L={L} partition_tokens={partition_tokens}", flush=True)
     big = Big(rkv, ctx, 1, [L - 1], cap=[L], seed=3)
     big.pool.alloc.reserve(0, L)
@@ -241,7 +245,8 @@ def test_fullsize_config3(rkv, rko, ctx, partition_tokens):
     for label, q in (("config3", q0), ("config3 outlier q", q1)):
         out = torch.empty((1, 1, HQ, D), dtype=torch.float32, device="cuda")
         _decode_step_check(rkv, rko, ctx, big, 0, [L], [0], q.float().cpu().numpy(), q, out,
-                           (kn, vn), partition_tokens=partition_tokens, label=label)
+                           (kn, vn), partition_tokens=partition_tokens, label=label,
+                           expect_pt=544 if partition_tokens == 0 else None)
     big.close()
 
 
