@@ -1053,22 +1053,35 @@ struct Decoder {
     for (int bl = 0; bl < kHB; ++bl) {
       const int blk = w * kHB + bl;
       const v4i sv = lds_load<v4i>(vs + 2 * (blk * 32 + 8 * lg));
+      // weights step by step across the eight pairs (see pv_weights), then
+      // both dim tiles' V operands, then the MFMAs: no MFMA reads a register
+      // the instruction just before it wrote
       v8h pb[2], pbl[2];
+      v2h prod[2][4], err[2][4];
 #pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
+      for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const v2h ph = __builtin_bit_cast(v2h, pq[nt][i]);
-          const v2h dv = __builtin_bit_cast(v2h, (uint32_t)sv[i]);
-          const v2h prod = ph * dv;
-          const v2h err = __builtin_elementwise_fma(ph, dv, -prod);
-          const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pq[nt][4 + i]), dv, err);
-          pb[nt][2 * i] = prod[0];
-          pb[nt][2 * i + 1] = prod[1];
+          prod[nt][i] = __builtin_bit_cast(v2h, pq[nt][i]) * __builtin_bit_cast(v2h, (uint32_t)sv[i]);
+          pb[nt][2 * i] = prod[nt][i][0];
+          pb[nt][2 * i + 1] = prod[nt][i][1];
+        }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          err[nt][i] = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pq[nt][i]),
+                                                 __builtin_bit_cast(v2h, (uint32_t)sv[i]), -prod[nt][i]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const v2h lo = __builtin_elementwise_fma(__builtin_bit_cast(v2h, pq[nt][4 + i]),
+                                                   __builtin_bit_cast(v2h, (uint32_t)sv[i]), err[nt][i]);
           pbl[nt][2 * i] = lo[0];
           pbl[nt][2 * i + 1] = lo[1];
         }
-      }
+      v8h va[2];
 #pragma unroll
       for (int hm = 0; hm < 2; ++hm) {
         const int d = 32 * blk + 16 * hm + li;
@@ -1078,14 +1091,16 @@ struct Decoder {
         v2h a0, a1, a2, a3;
         v8x4_to_f16(w0, a0, a1);
         v8x4_to_f16(w1, a2, a3);
-        const v8h va = {a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+        va[hm] = v8h{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+      }
+#pragma unroll
+      for (int hm = 0; hm < 2; ++hm)
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) {
           v4f &acc = oacc[0][nt * kHM + 2 * bl + hm];
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[nt], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pbl[nt], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[hm], pb[nt], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[hm], pbl[nt], acc, 0, 0, 0);
         }
-      }
     }
   }
 
