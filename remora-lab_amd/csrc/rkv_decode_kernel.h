@@ -354,7 +354,7 @@ struct Decoder {
   uint64_t PB;
   ChunkPlan<D, kSmall, kKReg, NW> plan;
   QOp kreg[2][kQC];        // kKReg: K codes of the tile being computed (A operands)
-  QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see load_q_planes)
+  QOp qhi[kQR][kQC], qmd[kQR][kQC], qlo[kQR][kQC];  // query planes (see split_q_planes)
   v8h qf[kQF];             // kF16K: query f16 operand per Q8 block (see load_q_f16)
   lds_u8 *kf16;            // kF16K: [token][D] f16, 16-byte chunk c of row r at c ^ (r & (D/8 - 1))
   const lds_u8 *ks;        // kPipe: the computed tile's K scales (copied out of its stage)
@@ -818,9 +818,9 @@ struct Decoder {
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          float v;
+          float v;  // unscaled: the softmax multiplies by rmul (> 0) in the fma below
           if constexpr (kWide) {
-            v = sacc[0][mt][r] * rmul[np];
+            v = sacc[0][mt][r];
           } else {
             // the even- and odd-block halves of a row sit 8 columns apart
             float lo_t = 0.f, hi_t = 0.f;
@@ -832,24 +832,27 @@ struct Decoder {
               else hi_t = tot;
             }
             // kColSplit: lanes li >= 8 hold row li - 8 (the ror-8 sum is symmetric)
-            v = (kColSplit || li < 8 ? lo_t : hi_t) * rmul[np];
+            v = kColSplit || li < 8 ? lo_t : hi_t;
           }
           s[4 * mt + r] = v;
           tmax = fmaxf(tmax, v);
         }
       if (!full) {
+        // token t0 + 16*mt + 4*lg + r is visible below rlim: compare the
+        // tile offset 16*mt + r with the lane's limit (immediates, one
+        // subtraction per tile)
+        const int32_t lim = (rlim[np] - 4 * lg) - t0;
         tmax = -INFINITY;
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int tok = t0 + 16 * mt + 4 * lg + r;
-            const float sv = tok < rlim[np] ? s[4 * mt + r] : -INFINITY;
+            const float sv = 16 * mt + r < lim ? s[4 * mt + r] : -INFINITY;
             s[4 * mt + r] = sv;
             tmax = fmaxf(tmax, sv);
           }
       }
-      tmax = row_group_max(tmax);
+      tmax = row_group_max(tmax) * rmul[np];  // max(s) * rmul = max(s * rmul), rmul > 0
       const bool need = tmax > mref[np] + kTau;  // also true for the first visible tile
       if (__any(need)) {
         const float mnew = need ? tmax : mref[np];
@@ -865,7 +868,7 @@ struct Decoder {
       float lsum = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        pr[e] = __builtin_amdgcn_exp2f(s[e] - muse);
+        pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], rmul[np], -muse));
         lsum += pr[e];
       }
       lrun[np] += lsum;
@@ -980,11 +983,12 @@ struct Decoder {
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float v = sown[mt][r] * rmul[0];
+        const float v = sown[mt][r];  // unscaled, as in compute
         s[4 * mt + r] = v;
         tmax = fmaxf(tmax, v);
       }
     if (!full) {
+      // compared by position (see mask_tail_scales)
       tmax = -INFINITY;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
@@ -996,7 +1000,7 @@ struct Decoder {
           tmax = fmaxf(tmax, sv);
         }
     }
-    tmax = row_group_max(tmax);
+    tmax = row_group_max(tmax) * rmul[0];
     const bool need = tmax > mref[0] + kTau;  // also true for the first visible tile
     float alpha = 1.0f;
     if (__any(need)) {
@@ -1012,7 +1016,7 @@ struct Decoder {
     float lsum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      pr[e] = __builtin_amdgcn_exp2f(s[e] - muse);
+      pr[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[e], rmul[0], -muse));
       lsum += pr[e];
     }
     lrun[0] += lsum;
@@ -1111,11 +1115,20 @@ struct Decoder {
   // every block; LDS accesses of a wave are performed in order, and the
   // waves of a workgroup that share the stage write the same values.
   __device__ __forceinline__ void mask_tail_scales(const lds_u8 *st, int32_t t0) {
+    // token t0 + 4*lg + k is kept when the tile offset k is below the
+    // lane's limit (kDSplit: compared by position; the limit would hold one
+    // more register across the loop, and that kernel has none to spare)
     uint32_t m[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int tk = t0 + (i < 2 ? 0 : 16) + 4 * lg + 2 * (i & 1);
-      m[i] = (tk < len ? 0xffffu : 0u) | (tk + 1 < len ? 0xffff0000u : 0u);
+      const int k = (i < 2 ? 0 : 16) + 2 * (i & 1);
+      if constexpr (kDSplit) {
+        const int tk = t0 + 4 * lg + k;
+        m[i] = (tk < len ? 0xffffu : 0u) | (tk + 1 < len ? 0xffff0000u : 0u);
+      } else {
+        const int32_t lim = (len - 4 * lg) - t0;
+        m[i] = (k < lim ? 0xffffu : 0u) | (k + 1 < lim ? 0xffff0000u : 0u);
+      }
     }
     if (li != 0) return;
 #pragma unroll
@@ -1598,6 +1611,15 @@ __device__ __forceinline__ void load_q_raw(const void *qp, bool bf16, int64_t qb
     }
   }
 }
+// The softmax multiplier of a query row stored as q * sign(scale) / sq:
+// |scale_log2| * sq, and at least FLT_MIN, so that it is positive (a zero
+// row or a zero scale gives scores of about 2^-80, i.e. a uniform softmax):
+// the softmax then takes the maximum of the unscaled scores and scales it
+// once, and every exponent is one fma of the unscaled score.
+__device__ __forceinline__ float softmax_mul(float amax, float sq, float scale_log2) {
+  return fmaxf(amax > 0.0f ? sq * fabsf(scale_log2) : 0.0f, 1.17549435e-38f);
+}
+
 template <int D>
 __device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][8], bool bf16, int li,
                                                int lg, float scale_log2, v4i *qhi, v4i *qmd,
@@ -1623,8 +1645,9 @@ __device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][8], 
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[c][e]));
   amax = fmaxf(amax, dpp_ror8(amax));  // the partner's half of the chunks
   amax = row_group_max(amax);
-  const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
-  qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
+  // a negative scale negates the planes (exact), so that qmul >= 0
+  const float inv = amax > 0.0f ? copysignf(16256.0f / amax, scale_log2) : 0.0f;
+  qmul = softmax_mul(amax, amax / 16256.0f, scale_log2);
   const bool live = (li < 8) == (lg < 2);
   const bool upper = li >= 8;  // this lane split elements 8..15
 #pragma unroll
@@ -1662,7 +1685,8 @@ __device__ __forceinline__ void split_q_planes(const uint32_t (&qw)[D / 64][8], 
 // that amax * 2^s lies in [2^14, 2^15): a bf16 value (8 significant bits)
 // times a power of two is then exact in f16 down to 2^-14, i.e. for every
 // element above amax * 2^-28, and the rest are within amax * 2^-39 of their
-// value.  qmul = scale_log2 * 2^-s undoes the scaling in the softmax.
+// value.  The row is negated for a negative scale, and qmul =
+// |scale_log2| * 2^-s (softmax_mul) undoes the scaling in the softmax.
 // kParts > 1: only blocks kPart*NB/kParts .. +NB/kParts-1 go to qf (the
 // scale still follows the whole row).
 template <int D, int kParts = 1, int kPart = 0>
@@ -1697,8 +1721,8 @@ __device__ __forceinline__ void load_q_f16(const uint16_t *qp, int64_t qbase, in
   int ex = 0;
   (void)frexpf(amax, &ex);  // amax = m * 2^ex, m in [0.5, 1)
   ex = max(ex, -111);       // keeps 2^(15 - ex) finite
-  const float sc = amax > 0.0f ? ldexpf(1.0f, 15 - ex) : 0.0f;
-  qmul = amax > 0.0f ? scale_log2 * ldexpf(1.0f, ex - 15) : 0.0f;
+  const float sc = amax > 0.0f ? copysignf(ldexpf(1.0f, 15 - ex), scale_log2) : 0.0f;
+  qmul = softmax_mul(amax, ldexpf(1.0f, ex - 15), scale_log2);
   constexpr int kNB = NB / kParts;
 #pragma unroll
   for (int b = 0; b < kNB; ++b)
@@ -1709,7 +1733,7 @@ __device__ __forceinline__ void load_q_f16(const uint16_t *qp, int64_t qbase, in
 // The query operands of the 16-row QK (Decoder::kWide): lane (li, lg) holds
 // row li's dims 32*blk + 8*lg .. +7 of every block blk, as the B operand of
 // v_mfma_i32_16x16x32_i8 (k = 8*lg .. 8*lg+7, column li); qbase < 0 is a
-// dead row (zeros).  Same planes and `qmul` as load_q_planes.
+// dead row (zeros).  Same planes and `qmul` as split_q_planes.
 template <int D>
 __device__ __forceinline__ void load_q_wide(const void *qp, bool bf16, int64_t qbase, int lg,
                                             float scale_log2, int64_t *qhi, int64_t *qmd,
@@ -1755,8 +1779,8 @@ __device__ __forceinline__ void load_q_wide(const void *qp, bool bf16, int64_t q
     for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(qv[b][e]));
   amax = fmaxf(amax, __shfl_xor(amax, 16));
   amax = fmaxf(amax, __shfl_xor(amax, 32));
-  const float inv = amax > 0.0f ? 16256.0f / amax : 0.0f;
-  qmul = amax > 0.0f ? (amax / 16256.0f) * scale_log2 : 0.0f;
+  const float inv = amax > 0.0f ? copysignf(16256.0f / amax, scale_log2) : 0.0f;
+  qmul = softmax_mul(amax, amax / 16256.0f, scale_log2);
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
     uint64_t h = 0, m = 0, l = 0;
@@ -2114,7 +2138,7 @@ __global__ __launch_bounds__(64 * NW, NW) void decode_kernel(DecodeLaunch p) {
     const int nt = Dec::kColSplit ? 0 : 2 * np + (li >> 3);
     // every lane of column li computed the scale of row 8*nt + (li & 7)
     // (kWide: of row li itself)
-    float mul = 0.0f;
+    float mul = 1.17549435e-38f;  // dead n-tiles: positive, as softmax_mul's
     if constexpr (Dec::kWide) {
       mul = qmul[0];
     } else {
