@@ -180,7 +180,9 @@ typedef struct rkv_decode_args {
   int32_t q_dtype;          /* RKV_F32 | RKV_BF16 */
   int32_t q_len;            /* 1 = decode; 2..4 = causal verify of draft rows */
   int32_t q_heads;          /* multiple of kv_heads (attention.rs:154-157) */
-  float scale;              /* softmax scale on q.k (1.0 = attention.rs) */
+  float scale;              /* softmax scale on q.k (1.0 = attention.rs); any finite
+                               value: negative reverses the score order, 0 gives a
+                               uniform softmax over the visible positions */
   void *out;                /* device [B][q_len][q_heads][head_dim] */
   int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
   int32_t partition_tokens; /* split-K partition length: a multiple of max(32,
@@ -229,7 +231,7 @@ typedef struct rkv_prefill_args {
   int32_t q_heads;          /* multiple of kv_heads, q_heads/kv_heads <= 128; a row
                                block takes floor(128/(q_heads/kv_heads)) chunk
                                tokens of all the kv head's q heads */
-  float scale;              /* softmax scale on q.k */
+  float scale;              /* softmax scale on q.k (any finite value, as in the decode) */
   void *out;                /* device [total_rows][q_heads][head_dim] */
   int32_t out_dtype;        /* RKV_F32 | RKV_BF16 */
   /* Split-K over the causal range (a row block's range in segments, merged
