@@ -115,3 +115,42 @@ def test_random_prefill_split_shapes(rkv, rko, ctx, seed):
     ent = [(i, c, n) for i, (c, n) in enumerate(ents)]
     P._run(rkv, rko, ctx, sc, ent, Hkv * G, 1.0 / math.sqrt(D), q_bf16=q_bf16, seed=seed,
            segment_tokens=seg)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_odd_group_shapes(rkv, rko, ctx, seed):
+    """GQA groups that are not powers of two (3, 5, 6, 7, 12 q heads per kv
+    head, so 3..28 rows per kv head with dead MFMA columns), a softmax scale
+    of random sign and magnitude, then a prefill over the same pages with the
+    same group (f32 or bf16 query, with or without the split workspace)."""
+    from tests import test_gpu_prefill as P
+    rng = np.random.default_rng(7000 + seed)
+    D = int(rng.choice([128, 256]))
+    PT = int(rng.choice([16, 32, 64, 128]))
+    Hkv = int(rng.choice([1, 2, 4]))
+    G = int(rng.choice([3, 5, 6, 7, 12]))
+    q_len = int(rng.choice([1, 2, 4]))
+    while q_len * G > 32:
+        q_len //= 2
+    B = int(rng.integers(1, 8))
+    lens = [max(int(rng.integers(1, 1200)), q_len) for _ in range(B)]
+    scale = float(rng.choice([-1.0, 1.0]) * rng.uniform(0.25, 2.0) / math.sqrt(D))
+    q_bf16 = bool(rng.random() < 0.5)
+    part = 0 if rng.random() < 0.5 else int(max(32, PT) * rng.integers(1, 5))
+    print(f"seed {seed}: D={D} PT={PT} Hkv={Hkv} G={G} q_len={q_len} lens={lens} scale={scale:+.4f} "
+          f"bf16 q={q_bf16} part={part}", flush=True)
+    sc = Scene(rkv, rko, Hkv, D, PT, lens, seed=seed, outliers=0.01, src_bf16=True)
+    q = rng.standard_normal((B, q_len, Hkv * G, D)).astype(np.float32)
+    if q_bf16:
+        q = rko.bf16_to_f32(rko.f32_to_bf16(q)).reshape(q.shape)
+    got, pt = _run_decode(rkv, ctx, sc, q, scale, q_bf16=q_bf16, q_len=q_len, partition_tokens=part)
+    want = rko.paged_decode(sc.lay, sc.pages, sc.bt, sc.lens, np.arange(B, dtype=np.int32), q,
+                            scale, pt)
+    assert_close(got, want, what=f"seed {seed} decode")
+    # prefill: each entry's last rows as a chunk after the rest of it
+    ents = []
+    for i, L in enumerate(lens):
+        n = int(rng.integers(1, min(L, 100) + 1))
+        ents.append((i, L - n, n))
+    seg = [None, 0][int(rng.integers(0, 2))]
+    P._run(rkv, rko, ctx, sc, ents, Hkv * G, scale, q_bf16=q_bf16, seed=seed, segment_tokens=seg)
