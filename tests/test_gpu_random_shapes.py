@@ -150,7 +150,7 @@ def test_random_odd_group_shapes(rkv, rko, ctx, seed):
     # prefill: each entry's last rows as a chunk after the rest of it
     ents = []
     for i, L in enumerate(lens):
-        n = int(rng.integers(1, min(L, 100) + 1))
+        n = int(rng.integers(1, min(L, 40) + 1))
         ents.append((i, L - n, n))
     seg = [None, 0][int(rng.integers(0, 2))]
     P._run(rkv, rko, ctx, sc, ents, Hkv * G, scale, q_bf16=q_bf16, seed=seed, segment_tokens=seg)
