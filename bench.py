@@ -393,7 +393,10 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "rkv::decode_kernel<256, 1, false, 2, 1, false>",
                      "achieved": round(dec_bytes / dec_s / 1e9, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(dec_bytes / dec_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(), "algorithmic_bytes_per_launch": dec_bytes},
+                     "traffic": read_traffic(), "algorithmic_bytes_per_launch": dec_bytes,
+                     "traffic_source": "profiles/decode_headline_pmc.txt: rocprofv3 --pmc FETCH_SIZE "
+                                       "and WRITE_SIZE of this kernel, scaled by a copy kernel's "
+                                       "counts (a separate profiled run, not this one)"},
     }
 
     # ---- practical ceiling: a plain streaming read of HBM in the same run ---------
